@@ -1,0 +1,163 @@
+// moe_align: stable counting sort of the routed (token, k) entries by expert.
+//
+// Restates deepseek_v4.py:155-164 (flatten, argsort, bincount, nonzero) with
+// the stable order (expert ascending, flat index ascending), and derives the
+// padded block layout used by the grouped GEMM: each expert's rows are padded
+// to a multiple of block_m so that an M block never straddles two experts.
+//
+// One workgroup of 1024 threads:
+//   1. LDS histogram (atomic increments; counts are order-independent).
+//   2. Three block-wide exclusive scans: unpadded offsets, padded offsets,
+//      active-expert ranks.
+//   3. Stable scatter in chunks of 1024 entries: within a wave, entries with
+//      the same expert are found by a ballot match over the key bits; the rank
+//      is the popcount of lower lanes; per-wave counts go through LDS to rank
+//      across the 16 waves; a running count per expert carries across chunks.
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+
+// exclusive scan of one int per thread across the workgroup; returns the total.
+__device__ int block_exclusive_scan(int v, int* lds_waves, int* out_total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int incl = v;
+  for (int o = 1; o < 64; o <<= 1) {
+    int t = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += t;
+  }
+  if (lane == 63) lds_waves[wave] = incl;
+  __syncthreads();
+  if (wave == 0) {
+    int w = (lane < kWaves) ? lds_waves[lane] : 0;
+    int wi = w;
+    for (int o = 1; o < 64; o <<= 1) {
+      int t = __shfl_up(wi, o, 64);
+      if (lane >= o) wi += t;
+    }
+    if (lane < kWaves) lds_waves[lane] = wi - w;
+    if (lane == kWaves - 1) *out_total = wi;
+  }
+  __syncthreads();
+  int r = lds_waves[wave] + incl - v;
+  __syncthreads();
+  return r;
+}
+
+template <typename IdT>
+__global__ __launch_bounds__(kThreads) void moe_align_kernel(const IdT* __restrict__ ids,
+                                                             const float* __restrict__ topk_w, int R, int K,
+                                                             int E, int block_m, int max_blocks,
+                                                             Dsv4AlignOut o) {
+  extern __shared__ int lds[];
+  int* cnt = lds;                    // [E + 1] (slot E collects out-of-range ids)
+  int* off_u = cnt + (E + 1);        // [E]
+  int* off_p = off_u + E;            // [E]
+  int* running = off_p + E;          // [E + 1]
+  int* wcount = running + (E + 1);   // [kWaves][E + 1]
+  __shared__ int scan_tmp[kWaves];
+  __shared__ int totals[3];
+  __shared__ int bad;
+
+  const int tid = threadIdx.x;
+  for (int i = tid; i < E + 1; i += kThreads) { cnt[i] = 0; running[i] = 0; }
+  for (int i = tid; i < kWaves * (E + 1); i += kThreads) wcount[i] = 0;
+  if (tid == 0) bad = 0;
+  __syncthreads();
+
+  // 1. histogram
+  for (int i = tid; i < R; i += kThreads) {
+    long long e = (long long)ids[i];
+    if (e < 0 || e >= E) { atomicAdd(&bad, 1); continue; }
+    atomicAdd(&cnt[(int)e], 1);
+  }
+  __syncthreads();
+
+  // 2. scans over experts (E <= kThreads)
+  const int c = (tid < E) ? cnt[tid] : 0;
+  const int padded = ((c + block_m - 1) / block_m) * block_m;
+  const int ou = block_exclusive_scan(c, scan_tmp, &totals[0]);
+  const int op = block_exclusive_scan(padded, scan_tmp, &totals[1]);
+  const int oa = block_exclusive_scan(c > 0 ? 1 : 0, scan_tmp, &totals[2]);
+  if (tid < E) {
+    off_u[tid] = ou;
+    off_p[tid] = op;
+    if (o.counts) o.counts[tid] = c;
+    if (o.expert_start) o.expert_start[tid] = op;
+    if (o.active) o.active[tid] = -1;
+  }
+  __syncthreads();
+  const int total_blocks = totals[1] / block_m;
+  if (tid < E) {
+    if (o.active && c > 0) o.active[oa] = tid;
+    const int b0 = op / block_m, b1 = min((op + padded) / block_m, max_blocks);
+    for (int b = b0; b < b1; ++b) o.block_expert[b] = tid;
+    const int p1 = min(op + padded, max_blocks * block_m);
+    for (int p = op + c; p < p1; ++p) o.sorted_ids[p] = R;  // padding sentinel
+  }
+  if (tid == 0) {
+    o.num_post_padded[0] = min(totals[1], max_blocks * block_m);
+    if (o.num_active) o.num_active[0] = totals[2];
+    if (o.status) o.status[0] = bad + (total_blocks > max_blocks ? (1 << 30) : 0);
+  }
+  __syncthreads();
+
+  // 3. stable scatter
+  const int lane = tid & 63, wave = tid >> 6;
+  int nbits = 0;
+  while ((1 << nbits) < E + 1) ++nbits;
+  const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int base = 0; base < R; base += kThreads) {
+    const int i = base + tid;
+    int e = E;
+    if (i < R) {
+      long long ee = (long long)ids[i];
+      if (ee >= 0 && ee < E) e = (int)ee;
+    }
+    unsigned long long peers = __ballot(1);
+    for (int b = 0; b < nbits; ++b) {
+      const int bit = (e >> b) & 1;
+      const unsigned long long bal = __ballot(bit);
+      peers &= bit ? bal : ~bal;
+    }
+    const int rank = __popcll(peers & lt_mask);
+    if (rank == 0) wcount[wave * (E + 1) + e] = __popcll(peers);
+    __syncthreads();
+    if (i < R && e < E) {
+      int r = running[e] + rank;
+      for (int w = 0; w < wave; ++w) r += wcount[w * (E + 1) + e];
+      const int u = off_u[e] + r;
+      const int p = off_p[e] + r;
+      if (o.order) o.order[u] = i;
+      if (o.s_e) o.s_e[u] = e;
+      if (o.s_w) o.s_w[u] = topk_w ? topk_w[i] : 0.0f;
+      if (o.row) o.row[u] = i / K;
+      if (p < max_blocks * block_m) o.sorted_ids[p] = i;
+      if (o.padded_pos) o.padded_pos[i] = p;
+    }
+    __syncthreads();
+    for (int ex = tid; ex < E + 1; ex += kThreads) {
+      int s = 0;
+      for (int w = 0; w < kWaves; ++w) { s += wcount[w * (E + 1) + ex]; wcount[w * (E + 1) + ex] = 0; }
+      running[ex] += s;
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace
+
+hipError_t launch_moe_align(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K, int E,
+                            int block_m, int max_blocks, const Dsv4AlignOut& o, hipStream_t st) {
+  const size_t lds = sizeof(int) * (size_t)((E + 1) + E + E + (E + 1) + kWaves * (E + 1));
+  if (ids_int64)
+    hipLaunchKernelGGL(moe_align_kernel<long long>, dim3(1), dim3(kThreads), lds, st,
+                       (const long long*)topk_ids, topk_w, R, K, E, block_m, max_blocks, o);
+  else
+    hipLaunchKernelGGL(moe_align_kernel<int32_t>, dim3(1), dim3(kThreads), lds, st,
+                       (const int32_t*)topk_ids, topk_w, R, K, E, block_m, max_blocks, o);
+  return hipGetLastError();
+}

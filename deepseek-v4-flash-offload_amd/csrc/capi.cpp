@@ -1,0 +1,308 @@
+// extern "C" entry points of libdsv4hip.so (declared in include/dsv4_moe.h).
+//
+// Every entry point validates its arguments on the host before anything is
+// launched, returns DSV4_OK or a negative status, and leaves a message for
+// dsv4_last_error(). Device buffers are owned by the caller; nothing here
+// allocates device memory except the slot manager (slots.cpp). Kernels are
+// enqueued on the caller's stream and nothing synchronises.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+#include <string>
+
+#include "common.h"
+#include "kernels.h"
+#include "../../include/dsv4_moe.h"
+
+static thread_local std::string g_last_error;
+
+int dsv4_fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+static int hip_status(hipError_t e, const char* where) {
+  if (e == hipSuccess) return DSV4_OK;
+  return dsv4_fail(DSV4_ERR_HIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+#define REQUIRE(cond, code, ...) \
+  do {                           \
+    if (!(cond)) return dsv4_fail(code, __VA_ARGS__); \
+  } while (0)
+
+static inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+static inline int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+extern "C" {
+
+const char* dsv4_last_error(void) { return g_last_error.c_str(); }
+
+int dsv4_abi_version(void) { return DSV4_ABI_VERSION; }
+
+// ---------------------------------------------------------------------------
+int dsv4_mxfp4_dequant_bf16(const void* packed, const void* scales, void* out, int64_t n_rows, int64_t k,
+                            void* stream) {
+  REQUIRE(n_rows >= 0 && k >= 0, DSV4_ERR_SHAPE, "dequant: negative size");
+  REQUIRE(k % 32 == 0, DSV4_ERR_SHAPE, "dequant: K=%lld must be a multiple of 32", (long long)k);
+  if (n_rows == 0 || k == 0) return DSV4_OK;
+  REQUIRE(packed && scales && out, DSV4_ERR_NULL, "dequant: null pointer");
+  REQUIRE(aligned(packed, 4) && aligned(out, 16), DSV4_ERR_SHAPE, "dequant: misaligned buffer");
+  return hip_status(launch_mxfp4_dequant((const uint8_t*)packed, (const uint8_t*)scales, (uint16_t*)out,
+                                         n_rows * k, (hipStream_t)stream),
+                    "dequant launch");
+}
+
+int dsv4_fp8_act_quant(const void* x, int64_t rows, int64_t cols, int block_size, void* rt, void* codes,
+                       void* scale_f32, void* scale_e8m0x4, void* stream) {
+  REQUIRE(rows >= 0 && cols >= 0, DSV4_ERR_SHAPE, "act_quant: negative size");
+  REQUIRE(block_size == 128, DSV4_ERR_UNSUPPORTED, "act_quant: block_size %d unsupported (128 only)", block_size);
+  REQUIRE(cols % block_size == 0, DSV4_ERR_SHAPE, "act_quant: last dim %lld not a multiple of %d",
+          (long long)cols, block_size);
+  if (rows == 0 || cols == 0) return DSV4_OK;
+  REQUIRE(x, DSV4_ERR_NULL, "act_quant: null input");
+  REQUIRE(rt || codes || scale_f32 || scale_e8m0x4, DSV4_ERR_NULL, "act_quant: no output requested");
+  REQUIRE(aligned(x, 16) && aligned(rt, 16) && aligned(codes, 8) && aligned(scale_e8m0x4, 4) &&
+              aligned(scale_f32, 4),
+          DSV4_ERR_SHAPE, "act_quant: misaligned buffer");
+  return hip_status(launch_fp8_act_quant((const uint16_t*)x, rows * cols, (uint16_t*)rt, (uint8_t*)codes,
+                                         (float*)scale_f32, (uint8_t*)scale_e8m0x4, (hipStream_t)stream),
+                    "act_quant launch");
+}
+
+int dsv4_mxfp4_act_quant(const void* x, int64_t rows, int64_t cols, int rule, void* packed, void* scale,
+                         void* dq, void* stream) {
+  REQUIRE(rows >= 0 && cols >= 0, DSV4_ERR_SHAPE, "mx_quant: negative size");
+  REQUIRE(rule == DSV4_RULE_CEIL_DIV6 || rule == DSV4_RULE_OCP_FLOOR, DSV4_ERR_UNSUPPORTED,
+          "mx_quant: unknown scale rule %d", rule);
+  REQUIRE(cols % 32 == 0, DSV4_ERR_SHAPE, "mx_quant: last dim %lld not a multiple of 32", (long long)cols);
+  if (rows == 0 || cols == 0) return DSV4_OK;
+  REQUIRE(x && packed && scale, DSV4_ERR_NULL, "mx_quant: null pointer");
+  REQUIRE(aligned(x, 16) && aligned(packed, 4) && aligned(dq, 16), DSV4_ERR_SHAPE, "mx_quant: misaligned buffer");
+  return hip_status(launch_mxfp4_act_quant((const uint16_t*)x, rows * cols, rule, (uint8_t*)packed,
+                                           (uint8_t*)scale, (uint16_t*)dq, (hipStream_t)stream),
+                    "mx_quant launch");
+}
+
+// ---------------------------------------------------------------------------
+int dsv4_moe_align_max_blocks(int R, int E, int block_m) {
+  if (R < 0 || E <= 0 || block_m <= 0) return dsv4_fail(DSV4_ERR_SHAPE, "align: bad sizes");
+  // sum_e ceil(c_e / B) <= R / B + #active <= R / B + min(E, R)
+  const int64_t nb = (int64_t)R / block_m + (R < E ? R : E) + 1;
+  return (int)nb;
+}
+
+int dsv4_moe_align(const void* topk_ids, int ids_int64, const float* topk_w, int T, int K, int E, int block_m,
+                   int max_blocks, int32_t* sorted_ids, int32_t* block_expert, int32_t* num_post_padded,
+                   int32_t* order, int32_t* s_e, float* s_w, int32_t* row, int32_t* counts,
+                   int32_t* expert_start, int32_t* active, int32_t* num_active, int32_t* padded_pos,
+                   int32_t* status, void* stream) {
+  REQUIRE(T >= 0 && K > 0, DSV4_ERR_SHAPE, "align: bad T=%d K=%d", T, K);
+  REQUIRE(E > 0 && E <= DSV4_MAX_EXPERTS, DSV4_ERR_UNSUPPORTED, "align: E=%d outside 1..%d", E,
+          DSV4_MAX_EXPERTS);
+  REQUIRE(block_m > 0 && block_m <= 1024, DSV4_ERR_SHAPE, "align: block_m=%d", block_m);
+  const int64_t R = (int64_t)T * K;
+  REQUIRE(R < (1 << 30), DSV4_ERR_SHAPE, "align: too many entries");
+  REQUIRE(max_blocks >= dsv4_moe_align_max_blocks((int)R, E, block_m), DSV4_ERR_SHAPE,
+          "align: max_blocks=%d below the bound %d", max_blocks, dsv4_moe_align_max_blocks((int)R, E, block_m));
+  REQUIRE(sorted_ids && block_expert && num_post_padded, DSV4_ERR_NULL, "align: null padded-layout output");
+  REQUIRE(R == 0 || topk_ids, DSV4_ERR_NULL, "align: null topk_ids");
+  Dsv4AlignOut o{sorted_ids, block_expert, num_post_padded, order, s_e, s_w, row, counts,
+                 expert_start, active, num_active, padded_pos, status};
+  return hip_status(launch_moe_align(topk_ids, ids_int64, topk_w, (int)R, K, E, block_m, max_blocks, o,
+                                     (hipStream_t)stream),
+                    "align launch");
+}
+
+int dsv4_moe_permute(const void* src, int64_t n_src, const int32_t* row, int64_t n_rows, int64_t row_bytes,
+                     void* dst, void* stream) {
+  REQUIRE(n_rows >= 0 && row_bytes >= 0 && n_src >= 0, DSV4_ERR_SHAPE, "permute: negative size");
+  REQUIRE(row_bytes % 16 == 0, DSV4_ERR_SHAPE, "permute: row bytes %lld not a multiple of 16",
+          (long long)row_bytes);
+  if (n_rows == 0 || row_bytes == 0) return DSV4_OK;
+  REQUIRE(src && row && dst, DSV4_ERR_NULL, "permute: null pointer");
+  REQUIRE(aligned(src, 16) && aligned(dst, 16), DSV4_ERR_SHAPE, "permute: misaligned buffer");
+  return hip_status(launch_moe_gather_rows((const uint8_t*)src, n_src, row, n_rows, row_bytes, (uint8_t*)dst,
+                                           (hipStream_t)stream),
+                    "permute launch");
+}
+
+int64_t dsv4_moe_unpermute_workspace_bytes(int T, int Kmax) {
+  return (int64_t)sizeof(int32_t) * ((int64_t)T + (int64_t)T * Kmax + 1);
+}
+
+int dsv4_moe_unpermute(const void* out_sorted, const int32_t* row, int R, int T, int Kmax, int D, void* workspace,
+                       void* y, void* stream) {
+  REQUIRE(R >= 0 && T >= 0 && D >= 0, DSV4_ERR_SHAPE, "unpermute: negative size");
+  REQUIRE(Kmax > 0 && Kmax <= DSV4_MAX_TOPK, DSV4_ERR_UNSUPPORTED, "unpermute: Kmax=%d outside 1..%d", Kmax,
+          DSV4_MAX_TOPK);
+  REQUIRE(D % 8 == 0, DSV4_ERR_SHAPE, "unpermute: D=%d not a multiple of 8", D);
+  if (T == 0 || D == 0) return DSV4_OK;
+  REQUIRE(workspace && y && (R == 0 || (out_sorted && row)), DSV4_ERR_NULL, "unpermute: null pointer");
+  REQUIRE(aligned(out_sorted, 16) && aligned(y, 16) && aligned(workspace, 4), DSV4_ERR_SHAPE,
+          "unpermute: misaligned buffer");
+  int32_t* cnt = (int32_t*)workspace;
+  int32_t* pos = cnt + T;
+  int32_t* status = pos + (int64_t)T * Kmax;
+  return hip_status(launch_moe_unpermute_rows((const uint16_t*)out_sorted, row, R, T, Kmax, D, cnt, pos, status,
+                                              (uint16_t*)y, (hipStream_t)stream),
+                    "unpermute launch");
+}
+
+int dsv4_moe_combine(const void* out_flat, const void* topk_ids, int ids_int64, int T, int K, int D, void* y,
+                     void* stream) {
+  REQUIRE(T >= 0 && D >= 0, DSV4_ERR_SHAPE, "combine: negative size");
+  REQUIRE(K > 0 && K <= DSV4_MAX_TOPK, DSV4_ERR_UNSUPPORTED, "combine: K=%d outside 1..%d", K, DSV4_MAX_TOPK);
+  REQUIRE(D % 8 == 0, DSV4_ERR_SHAPE, "combine: D=%d not a multiple of 8", D);
+  if (T == 0 || D == 0) return DSV4_OK;
+  REQUIRE(out_flat && topk_ids && y, DSV4_ERR_NULL, "combine: null pointer");
+  REQUIRE(aligned(out_flat, 16) && aligned(y, 16), DSV4_ERR_SHAPE, "combine: misaligned buffer");
+  return hip_status(launch_moe_combine_flat((const uint16_t*)out_flat, topk_ids, ids_int64, T, K, D,
+                                            (uint16_t*)y, (hipStream_t)stream),
+                    "combine launch");
+}
+
+// ---------------------------------------------------------------------------
+static int check_gemm_common(int afmt, const void* a, const void* a_scale, const int32_t* sorted_ids,
+                             const int32_t* block_expert, const int32_t* npp, int R, int max_blocks,
+                             const void* experts, int Kdim, void* out) {
+  REQUIRE(afmt == DSV4_AFMT_E4M3 || afmt == DSV4_AFMT_E2M1, DSV4_ERR_UNSUPPORTED, "gemm: unknown A format %d",
+          afmt);
+  REQUIRE(R >= 0 && max_blocks >= 0, DSV4_ERR_SHAPE, "gemm: negative size");
+  REQUIRE(Kdim > 0 && Kdim % 512 == 0, DSV4_ERR_UNSUPPORTED, "gemm: reduction dim %d not a multiple of 512",
+          Kdim);
+  REQUIRE(a && a_scale && sorted_ids && block_expert && npp && experts && out, DSV4_ERR_NULL,
+          "gemm: null pointer");
+  REQUIRE(aligned(a, 16) && aligned(a_scale, 4) && aligned(experts, 8), DSV4_ERR_SHAPE,
+          "gemm: misaligned buffer");
+  return DSV4_OK;
+}
+
+int dsv4_moe_gemm_gateup(int afmt, const void* a, const void* a_scale, int a_row_div, const int32_t* sorted_ids,
+                         const int32_t* block_expert, const int32_t* num_post_padded, int R, int block_m,
+                         int max_blocks, const void* expert_table, int D, int I, const float* topk_w,
+                         float swiglu_limit, void* h_out, void* stream) {
+  REQUIRE(block_m == DSV4_GEMM_BLOCK_M, DSV4_ERR_UNSUPPORTED, "gemm: block_m %d unsupported (%d)", block_m,
+          DSV4_GEMM_BLOCK_M);
+  REQUIRE(I > 0 && I % 64 == 0, DSV4_ERR_UNSUPPORTED, "gemm gate/up: I=%d not a multiple of 64", I);
+  REQUIRE(a_row_div > 0, DSV4_ERR_SHAPE, "gemm gate/up: a_row_div=%d", a_row_div);
+  if (R == 0 || max_blocks == 0) return DSV4_OK;
+  int rc = check_gemm_common(afmt, a, a_scale, sorted_ids, block_expert, num_post_padded, R, max_blocks,
+                             expert_table, D, h_out);
+  if (rc) return rc;
+  REQUIRE(topk_w, DSV4_ERR_NULL, "gemm gate/up: null routing weights");
+  Dsv4GemmArgs g{afmt, (const uint8_t*)a, afmt == DSV4_AFMT_E4M3 ? (int64_t)D : (int64_t)D / 2,
+                 (const uint8_t*)a_scale, a_row_div, sorted_ids, block_expert, num_post_padded, R, block_m,
+                 max_blocks, (const Dsv4ExpertPtrs*)expert_table, D, I, topk_w, swiglu_limit,
+                 (uint16_t*)h_out};
+  return hip_status(launch_moe_gemm_gateup(g, (hipStream_t)stream), "gemm gate/up launch");
+}
+
+int dsv4_moe_gemm_down(int afmt, const void* a, const void* a_scale, const int32_t* sorted_ids,
+                       const int32_t* block_expert, const int32_t* num_post_padded, int R, int block_m,
+                       int max_blocks, const void* expert_table, int I, int D, void* out, void* stream) {
+  REQUIRE(block_m == DSV4_GEMM_BLOCK_M, DSV4_ERR_UNSUPPORTED, "gemm: block_m %d unsupported (%d)", block_m,
+          DSV4_GEMM_BLOCK_M);
+  REQUIRE(D > 0 && D % 128 == 0, DSV4_ERR_UNSUPPORTED, "gemm down: D=%d not a multiple of 128", D);
+  if (R == 0 || max_blocks == 0) return DSV4_OK;
+  int rc = check_gemm_common(afmt, a, a_scale, sorted_ids, block_expert, num_post_padded, R, max_blocks,
+                             expert_table, I, out);
+  if (rc) return rc;
+  Dsv4GemmArgs g{afmt, (const uint8_t*)a, afmt == DSV4_AFMT_E4M3 ? (int64_t)I : (int64_t)I / 2,
+                 (const uint8_t*)a_scale, 1, sorted_ids, block_expert, num_post_padded, R, block_m, max_blocks,
+                 (const Dsv4ExpertPtrs*)expert_table, I, D, nullptr, 0.0f, (uint16_t*)out};
+  return hip_status(launch_moe_gemm_down(g, (hipStream_t)stream), "gemm down launch");
+}
+
+// ---------------------------------------------------------------------------
+// Fused routed layer: align -> activation quant -> gate/up GEMM + SwiGLU ->
+// h quant -> down GEMM -> combine. Workspace regions are 256-byte aligned.
+struct LayerWs {
+  int64_t sorted_ids, block_expert, npp, status, xa, xs, h, ha, hs, out, total;
+  int max_blocks;
+};
+
+static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile) {
+  LayerWs w{};
+  const int64_t R = (int64_t)T * K;
+  const int bm = DSV4_GEMM_BLOCK_M;
+  w.max_blocks = dsv4_moe_align_max_blocks((int)R, E, bm);
+  const bool fp8 = profile == DSV4_PROFILE_BF16;
+  int64_t o = 0;
+  auto take = [&](int64_t bytes) { int64_t at = o; o = round_up(o + bytes, 256); return at; };
+  w.sorted_ids = take(sizeof(int32_t) * (int64_t)w.max_blocks * bm);
+  w.block_expert = take(sizeof(int32_t) * (int64_t)w.max_blocks);
+  w.npp = take(sizeof(int32_t));
+  w.status = take(sizeof(int32_t));
+  w.xa = take(fp8 ? (int64_t)T * D : (int64_t)T * D / 2);
+  w.xs = take((int64_t)T * D / 32);
+  w.h = take(2 * R * I);
+  w.ha = take(fp8 ? R * I : R * I / 2);
+  w.hs = take(R * I / 32);
+  w.out = take(2 * R * D);
+  w.total = o;
+  return w;
+}
+
+int dsv4_moe_layer_workspace_bytes(int T, int K, int E, int D, int I, int profile, int64_t* bytes) {
+  REQUIRE(bytes, DSV4_ERR_NULL, "workspace: null output");
+  REQUIRE(T >= 0 && K > 0 && E > 0 && D > 0 && I > 0, DSV4_ERR_SHAPE, "workspace: bad sizes");
+  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4, DSV4_ERR_UNSUPPORTED,
+          "workspace: unknown profile %d", profile);
+  *bytes = layer_ws(T, K, E, D, I, profile).total;
+  return DSV4_OK;
+}
+
+int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
+                           const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
+                           float swiglu_limit, void* workspace, int64_t workspace_bytes, void* y, void* stream) {
+  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4, DSV4_ERR_UNSUPPORTED,
+          "layer: unknown profile %d", profile);
+  REQUIRE(T >= 0 && K > 0 && K <= DSV4_MAX_TOPK, DSV4_ERR_SHAPE, "layer: bad T=%d K=%d", T, K);
+  REQUIRE(D % 512 == 0 && I % 512 == 0 && D > 0 && I > 0, DSV4_ERR_UNSUPPORTED,
+          "layer: D=%d and I=%d must be multiples of 512", D, I);
+  if (T == 0) return DSV4_OK;
+  REQUIRE(x && topk_ids && topk_w && expert_table && workspace && y, DSV4_ERR_NULL, "layer: null pointer");
+  const LayerWs w = layer_ws(T, K, E, D, I, profile);
+  REQUIRE(workspace_bytes >= w.total, DSV4_ERR_SHAPE, "layer: workspace %lld < %lld bytes",
+          (long long)workspace_bytes, (long long)w.total);
+  REQUIRE(aligned(workspace, 256), DSV4_ERR_SHAPE, "layer: workspace not 256-byte aligned");
+  char* base = (char*)workspace;
+  int32_t* sorted_ids = (int32_t*)(base + w.sorted_ids);
+  int32_t* block_expert = (int32_t*)(base + w.block_expert);
+  int32_t* npp = (int32_t*)(base + w.npp);
+  int32_t* status = (int32_t*)(base + w.status);
+  const int R = T * K;
+  const int bm = DSV4_GEMM_BLOCK_M;
+  int rc = dsv4_moe_align(topk_ids, ids_int64, nullptr, T, K, E, bm, w.max_blocks, sorted_ids, block_expert, npp,
+                          nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, status,
+                          stream);
+  if (rc) return rc;
+  const bool fp8 = profile == DSV4_PROFILE_BF16;
+  const int afmt = fp8 ? DSV4_AFMT_E4M3 : DSV4_AFMT_E2M1;
+  if (fp8)
+    rc = dsv4_fp8_act_quant(x, T, D, 128, nullptr, base + w.xa, nullptr, base + w.xs, stream);
+  else
+    rc = dsv4_mxfp4_act_quant(x, T, D, scale_rule, base + w.xa, base + w.xs, nullptr, stream);
+  if (rc) return rc;
+  rc = dsv4_moe_gemm_gateup(afmt, base + w.xa, base + w.xs, K, sorted_ids, block_expert, npp, R, bm, w.max_blocks,
+                            expert_table, D, I, topk_w, swiglu_limit, base + w.h, stream);
+  if (rc) return rc;
+  if (fp8)
+    rc = dsv4_fp8_act_quant(base + w.h, R, I, 128, nullptr, base + w.ha, nullptr, base + w.hs, stream);
+  else
+    rc = dsv4_mxfp4_act_quant(base + w.h, R, I, scale_rule, base + w.ha, base + w.hs, nullptr, stream);
+  if (rc) return rc;
+  rc = dsv4_moe_gemm_down(afmt, base + w.ha, base + w.hs, sorted_ids, block_expert, npp, R, bm, w.max_blocks,
+                          expert_table, I, D, base + w.out, stream);
+  if (rc) return rc;
+  return dsv4_moe_combine(base + w.out, topk_ids, ids_int64, T, K, D, y, stream);
+}
+
+}  // extern "C"

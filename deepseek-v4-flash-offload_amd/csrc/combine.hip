@@ -1,0 +1,145 @@
+// Row gather (permute) and the deterministic unweighted combine (unpermute).
+//
+// permute   : x_sorted = x[row]           (deepseek_v4.py:171, 213-214)
+// unpermute : y = zeros(fp32); y.index_add_(0, row, out.float()); y.bf16()
+//             (deepseek_v4.py:195-197, 243-245)
+// index_add_ accumulates each token's rows in ascending sorted position, which
+// for the routed layout is ascending expert id. The combine below sums every
+// token's rows in that order starting from +0.0f, one workgroup per token and
+// no atomics, so the result is bit-identical to the reference's fp32 sum.
+#include "common.h"
+#include "kernels.h"
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Rows whose index is outside [0, n_src) are written as zeros.
+__global__ __launch_bounds__(256) void gather_rows_kernel(const u32x4* __restrict__ src,
+                                                          const int32_t* __restrict__ row, int64_t n_src,
+                                                          int64_t n_rows, int64_t row_vecs,
+                                                          u32x4* __restrict__ dst) {
+  const int64_t total = n_rows * row_vecs;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t r = i / row_vecs, c = i - r * row_vecs;
+    const int64_t sr = row[r];
+    dst[i] = (sr >= 0 && sr < n_src) ? src[sr * row_vecs + c] : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+constexpr int kMaxK = 32;
+
+DSV4_DEV void accumulate8(float* acc, u32x4 v) {
+  acc[0] += dsv4::bf16_to_f32(v.x & 0xffffu); acc[1] += dsv4::bf16_to_f32(v.x >> 16);
+  acc[2] += dsv4::bf16_to_f32(v.y & 0xffffu); acc[3] += dsv4::bf16_to_f32(v.y >> 16);
+  acc[4] += dsv4::bf16_to_f32(v.z & 0xffffu); acc[5] += dsv4::bf16_to_f32(v.z >> 16);
+  acc[6] += dsv4::bf16_to_f32(v.w & 0xffffu); acc[7] += dsv4::bf16_to_f32(v.w >> 16);
+}
+
+DSV4_DEV u32x4 pack8(const float* acc) {
+  u32x4 r;
+  r.x = dsv4::f32_to_bf16(acc[0]) | (dsv4::f32_to_bf16(acc[1]) << 16);
+  r.y = dsv4::f32_to_bf16(acc[2]) | (dsv4::f32_to_bf16(acc[3]) << 16);
+  r.z = dsv4::f32_to_bf16(acc[4]) | (dsv4::f32_to_bf16(acc[5]) << 16);
+  r.w = dsv4::f32_to_bf16(acc[6]) | (dsv4::f32_to_bf16(acc[7]) << 16);
+  return r;
+}
+
+// One workgroup per token. The token's K entries are ordered by (key, k) with
+// an insertion sort that every thread performs identically.
+template <typename IdT>
+__global__ __launch_bounds__(256) void combine_flat_kernel(const u32x4* __restrict__ src,
+                                                           const IdT* __restrict__ ids, int K, int D,
+                                                           u32x4* __restrict__ y) {
+  const int t = blockIdx.x;
+  int ord[kMaxK];
+  long long key[kMaxK];
+  for (int k = 0; k < K; ++k) {
+    long long kk = (long long)ids[(int64_t)t * K + k];
+    int j = k;
+    while (j > 0 && key[j - 1] > kk) { key[j] = key[j - 1]; ord[j] = ord[j - 1]; --j; }
+    key[j] = kk; ord[j] = k;
+  }
+  const int vecs = D / 8;
+  for (int c = threadIdx.x; c < vecs; c += 256) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < K; ++j) accumulate8(acc, src[((int64_t)t * K + ord[j]) * vecs + c]);
+    y[(int64_t)t * vecs + c] = pack8(acc);
+  }
+}
+
+__global__ __launch_bounds__(256) void bucket_rows_kernel(const int32_t* __restrict__ row, int R, int T, int Kmax,
+                                                          int32_t* __restrict__ cnt, int32_t* __restrict__ pos,
+                                                          int32_t* __restrict__ status) {
+  const int u = blockIdx.x * 256 + threadIdx.x;
+  if (u >= R) return;
+  const int t = row[u];
+  if (t < 0 || t >= T) { atomicAdd(status, 1); return; }
+  const int s = atomicAdd(&cnt[t], 1);
+  if (s < Kmax) pos[(int64_t)t * Kmax + s] = u; else atomicAdd(status, 1);
+}
+
+__global__ __launch_bounds__(256) void zero_i32_kernel(int32_t* p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+__global__ __launch_bounds__(256) void combine_rows_kernel(const u32x4* __restrict__ src,
+                                                           const int32_t* __restrict__ cnt,
+                                                           const int32_t* __restrict__ pos, int Kmax, int D,
+                                                           u32x4* __restrict__ y) {
+  const int t = blockIdx.x;
+  const int n = min(cnt[t], Kmax);
+  int p[kMaxK];
+  for (int k = 0; k < n; ++k) {
+    int v = pos[(int64_t)t * Kmax + k];
+    int j = k;
+    while (j > 0 && p[j - 1] > v) { p[j] = p[j - 1]; --j; }
+    p[j] = v;
+  }
+  const int vecs = D / 8;
+  for (int c = threadIdx.x; c < vecs; c += 256) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < n; ++j) accumulate8(acc, src[(int64_t)p[j] * vecs + c]);
+    y[(int64_t)t * vecs + c] = pack8(acc);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_moe_gather_rows(const uint8_t* src, int64_t n_src, const int32_t* row, int64_t n_rows,
+                                  int64_t row_bytes, uint8_t* dst, hipStream_t st) {
+  const int64_t vecs = row_bytes / 16;
+  const int64_t total = n_rows * vecs;
+  if (total == 0) return hipSuccess;
+  int64_t want = (total + 255) / 256;
+  hipLaunchKernelGGL(gather_rows_kernel, dim3((int)(want < 16384 ? want : 16384)), dim3(256), 0, st,
+                     (const u32x4*)src, row, n_src, n_rows, vecs, (u32x4*)dst);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_combine_flat(const uint16_t* src, const void* topk_ids, int ids_int64, int T, int K,
+                                   int D, uint16_t* y, hipStream_t st) {
+  if (T == 0) return hipSuccess;
+  if (ids_int64)
+    hipLaunchKernelGGL(combine_flat_kernel<long long>, dim3(T), dim3(256), 0, st, (const u32x4*)src,
+                       (const long long*)topk_ids, K, D, (u32x4*)y);
+  else
+    hipLaunchKernelGGL(combine_flat_kernel<int32_t>, dim3(T), dim3(256), 0, st, (const u32x4*)src,
+                       (const int32_t*)topk_ids, K, D, (u32x4*)y);
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_unpermute_rows(const uint16_t* src, const int32_t* row, int R, int T, int Kmax, int D,
+                                     int32_t* work_cnt, int32_t* work_pos, int32_t* status, uint16_t* y,
+                                     hipStream_t st) {
+  if (T == 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_i32_kernel, dim3((T + 255) / 256), dim3(256), 0, st, work_cnt, T);
+  hipLaunchKernelGGL(zero_i32_kernel, dim3(1), dim3(256), 0, st, status, 1);
+  if (R > 0)
+    hipLaunchKernelGGL(bucket_rows_kernel, dim3((R + 255) / 256), dim3(256), 0, st, row, R, T, Kmax, work_cnt,
+                       work_pos, status);
+  hipLaunchKernelGGL(combine_rows_kernel, dim3(T), dim3(256), 0, st, (const u32x4*)src, work_cnt, work_pos,
+                     Kmax, D, (u32x4*)y);
+  return hipGetLastError();
+}

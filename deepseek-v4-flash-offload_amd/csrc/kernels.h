@@ -1,0 +1,73 @@
+// Internal launcher declarations shared between the kernel files and the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+// Per-expert device pointers of one expert's packed MXFP4 weights, in the
+// checkpoint layout: w1/w3 [I, D/2] + [I, D/32], w2 [D, I/2] + [D, I/32].
+struct Dsv4ExpertPtrs {
+  const uint8_t* w1p;
+  const uint8_t* w1s;
+  const uint8_t* w2p;
+  const uint8_t* w2s;
+  const uint8_t* w3p;
+  const uint8_t* w3s;
+};
+
+hipError_t launch_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, uint16_t* out,
+                                int64_t n_elems, hipStream_t st);
+hipError_t launch_fp8_act_quant(const uint16_t* x, int64_t n_elems, uint16_t* rt, uint8_t* codes,
+                                float* scale_f32, uint8_t* scale_e8m0x4, hipStream_t st);
+hipError_t launch_mxfp4_act_quant(const uint16_t* x, int64_t n_elems, int rule, uint8_t* packed,
+                                  uint8_t* scale, uint16_t* dq, hipStream_t st);
+
+struct Dsv4AlignOut {
+  int32_t* sorted_ids;          // [max_blocks * block_m] flat index per padded slot, R = pad
+  int32_t* block_expert;        // [max_blocks]
+  int32_t* num_post_padded;     // [1]
+  int32_t* order;               // [R] (nullable) stable argsort of flat expert ids
+  int32_t* s_e;                 // [R] (nullable)
+  float* s_w;                   // [R] (nullable)
+  int32_t* row;                 // [R] (nullable)
+  int32_t* counts;              // [E] (nullable)
+  int32_t* expert_start;        // [E] (nullable) first padded slot
+  int32_t* active;              // [E] (nullable) active experts ascending, -1 tail
+  int32_t* num_active;          // [1] (nullable)
+  int32_t* padded_pos;          // [R] (nullable) padded slot of each flat index
+  int32_t* status;              // [1] (nullable) count of out-of-range expert ids
+};
+hipError_t launch_moe_align(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K,
+                            int E, int block_m, int max_blocks, const Dsv4AlignOut& o, hipStream_t st);
+
+hipError_t launch_moe_gather_rows(const uint8_t* src, int64_t n_src, const int32_t* row, int64_t n_rows,
+                                  int64_t row_bytes, uint8_t* dst, hipStream_t st);
+// y[t] = bf16( sum over the token's entries, ordered by key, of rows of `src` (bf16) )
+// mode 0: entry (t,k) -> src row t*K+k, key = topk_ids[t,k]   (flat-order combine)
+// mode 1: entries from a per-token position list built from `row`, key = position
+hipError_t launch_moe_combine_flat(const uint16_t* src, const void* topk_ids, int ids_int64, int T, int K,
+                                   int D, uint16_t* y, hipStream_t st);
+hipError_t launch_moe_unpermute_rows(const uint16_t* src, const int32_t* row, int R, int T, int Kmax, int D,
+                                     int32_t* work_cnt, int32_t* work_pos, int32_t* status, uint16_t* y,
+                                     hipStream_t st);
+
+struct Dsv4GemmArgs {
+  int afmt;                       // 0: A is E4M3 codes (1 byte/elt); 1: A is packed E2M1 (2 elts/byte)
+  const uint8_t* a;               // A codes, row-major
+  int64_t a_row_bytes;
+  const uint8_t* a_scale;         // E8M0 byte per 32 A elements, row-major [rows, Kdim/32]
+  int a_row_div;                  // A row = flat_index / a_row_div (K of top-k for the gate/up GEMM, 1 for down)
+  const int32_t* sorted_ids;      // padded slots -> flat index; >= R means padding
+  const int32_t* block_expert;    // expert of each M block
+  const int32_t* num_post_padded; // device scalar
+  int R;
+  int block_m;
+  int max_blocks;
+  const Dsv4ExpertPtrs* experts;  // device table indexed by expert id
+  int Kdim;                       // reduction length
+  int N;                          // output columns (I for gate/up, D for down)
+  const float* topk_w;            // [R] routing weight by flat index (gate/up only)
+  float swiglu_limit;             // <= 0 disables the clamp
+  uint16_t* out;                  // bf16 [R, N] by flat index
+};
+hipError_t launch_moe_gemm_gateup(const Dsv4GemmArgs& a, hipStream_t st);
+hipError_t launch_moe_gemm_down(const Dsv4GemmArgs& a, hipStream_t st);

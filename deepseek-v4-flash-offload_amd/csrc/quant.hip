@@ -1,0 +1,221 @@
+// MXFP4 weight dequant, FP8 activation round trip and MXFP4 activation quant.
+//
+// All three are HBM-bound streaming kernels: one thread owns 8 consecutive
+// elements (16 B of bf16), consecutive lanes own consecutive 8-element groups,
+// so every load and store instruction of a wave covers one contiguous span.
+#include "common.h"
+#include "kernels.h"
+
+using namespace dsv4;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// MXFP4 weight -> bf16 (npu_ops.py:142-158).
+// Group g = 8 elements = packed dword g; its scale is byte g/4 (32 elements per
+// scale). The hardware scaled convert produces LUT[nibble] * 2^(s-127) rounded
+// to bf16, which equals the reference's fp32 product (exact: <= 2 significant
+// bits) except for nibble 8, which the hardware decodes to -0.0 (the reference
+// table holds +0.0), and for scale byte 255, where the reference multiplies by
+// +inf. Both are corrected here.
+// ---------------------------------------------------------------------------
+DSV4_DEV uint32_t fix_neg_zero(uint32_t r) {
+  uint32_t t = r & 0x7fff7fffu;
+  uint32_t nz = (t + 0x7fff7fffu) & 0x80008000u;  // bit 15 of a half set iff that half != +-0
+  return r & (0x7fff7fffu | nz);
+}
+
+DSV4_DEV uint32_t inf_scale_pair(uint32_t byte) {
+  uint32_t r = 0;
+  for (int h = 0; h < 2; ++h) {
+    uint32_t nib = (byte >> (4 * h)) & 15u;
+    uint32_t v = ((nib & 7u) == 0) ? 0x7fc0u : ((nib & 8u) ? 0xff80u : 0x7f80u);
+    r |= v << (16 * h);
+  }
+  return r;
+}
+
+DSV4_DEV u32x4 dequant8(uint32_t p, uint32_t s) {
+  float sc = e8m0_to_f32(s);
+  u32x4 r;
+  r.x = fix_neg_zero(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc, 0)));
+  r.y = fix_neg_zero(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc, 1)));
+  r.z = fix_neg_zero(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc, 2)));
+  r.w = fix_neg_zero(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(p, sc, 3)));
+  if (s == 255u) {
+    r.x = inf_scale_pair(p & 0xffu);
+    r.y = inf_scale_pair((p >> 8) & 0xffu);
+    r.z = inf_scale_pair((p >> 16) & 0xffu);
+    r.w = inf_scale_pair(p >> 24);
+  }
+  return r;
+}
+
+__global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint32_t* __restrict__ packed,
+                                                             const uint8_t* __restrict__ scales,
+                                                             u32x4* __restrict__ out, int64_t n_groups) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  // four independent groups in flight per thread
+  for (; g + 3 * stride < n_groups; g += 4 * stride) {
+    uint32_t p0 = __builtin_nontemporal_load(packed + g);
+    uint32_t p1 = __builtin_nontemporal_load(packed + g + stride);
+    uint32_t p2 = __builtin_nontemporal_load(packed + g + 2 * stride);
+    uint32_t p3 = __builtin_nontemporal_load(packed + g + 3 * stride);
+    uint32_t s0 = scales[g >> 2], s1 = scales[(g + stride) >> 2];
+    uint32_t s2 = scales[(g + 2 * stride) >> 2], s3 = scales[(g + 3 * stride) >> 2];
+    u32x4 r0 = dequant8(p0, s0), r1 = dequant8(p1, s1), r2 = dequant8(p2, s2), r3 = dequant8(p3, s3);
+    __builtin_nontemporal_store(r0, out + g);
+    __builtin_nontemporal_store(r1, out + g + stride);
+    __builtin_nontemporal_store(r2, out + g + 2 * stride);
+    __builtin_nontemporal_store(r3, out + g + 3 * stride);
+  }
+  for (; g < n_groups; g += stride) out[g] = dequant8(packed[g], scales[g >> 2]);
+}
+
+// ---------------------------------------------------------------------------
+// act_quant (npu_ops.py:73-104): per-128 block of one row,
+//   amax = max(max|x|, 1e-4); s = 2^ceil(log2(max(amax * fp32(1/448), 2^-126)))
+//   code = e4m3fn(clamp(x / s, +-448)) (RNE); rt = bf16(e4m3(code) * s)
+// 16 lanes own one block (8 elements each).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void fp8_act_quant_kernel(const uint4* __restrict__ x, int64_t n_groups,
+                                                             uint4* __restrict__ rt, uint2* __restrict__ codes,
+                                                             float* __restrict__ scale_f32,
+                                                             uint32_t* __restrict__ scale_e8m0x4) {
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const bool live = g < n_groups;  // n_groups is a multiple of 16, so whole blocks share liveness
+  uint4 v = live ? x[g] : make_uint4(0, 0, 0, 0);
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  float f[8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_to_f32(w[i] & 0xffffu);
+    f[2 * i + 1] = bf16_to_f32(w[i] >> 16);
+    amax = fmaxf(amax, fmaxf(fabsf(f[2 * i]), fabsf(f[2 * i + 1])));
+  }
+  amax = wave_max_xor(amax, 16);
+  amax = fmaxf(amax, 1e-4f);
+  float vs = fmaxf(amax * (1.0f / 448.0f), 1.1754943508222875e-38f);
+  int k = ceil_log2(vs);
+  float s = pow2f(k), inv = pow2f(-k);
+  uint32_t c[8];
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float y = fminf(fmaxf(f[i] * inv, -448.0f), 448.0f);
+    uint32_t neg = __float_as_uint(y) >> 31;
+    uint32_t mag = e4m3_mag_code(fabsf(y));
+    c[i] = mag | (neg << 7);
+    float q = e4m3_mag_value(mag) * s;
+    uint32_t b = f32_to_bf16(neg ? -q : q);
+    if (i & 1) o[i >> 1] |= b << 16; else o[i >> 1] = b;
+  }
+  if (!live) return;
+  if (rt) rt[g] = make_uint4(o[0], o[1], o[2], o[3]);
+  if (codes) codes[g] = make_uint2(c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24),
+                                   c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24));
+  if ((threadIdx.x & 15) == 0) {
+    const int64_t blk = g >> 4;
+    if (scale_f32) scale_f32[blk] = s;
+    if (scale_e8m0x4) scale_e8m0x4[blk] = (uint32_t)(k + 127) * 0x01010101u;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// MXFP4 activation quant, per 32 elements; 4 lanes own one block.
+//  rule 0 "ceil_div6" (npu_ops.py:107-121):
+//     amax = max(max|x|, 6*2^-126); s = 2^ceil(log2(max(amax*fp32(1/6), 2^-126)))
+//     v = clamp(x/s, +-6); q = E2M1-RNE(|v|); sign = (v < 0); dq = bf16(+-q * s)
+//  rule 1 "ocp_floor" (OCP MX v1.0): shared = floor(log2 amax) - 2 clamped to
+//     [-127, 127] (-127 for an all-zero block); q = E2M1-RNE(min(|x|/2^shared, 6));
+//     sign = signbit(x)
+// Outputs: packed nibbles (low = even element), E8M0 scale byte, optional bf16 dq.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mxfp4_act_quant_kernel(const uint4* __restrict__ x, int64_t n_groups,
+                                                               int rule, uint32_t* __restrict__ packed,
+                                                               uint8_t* __restrict__ scale,
+                                                               uint4* __restrict__ dq) {
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const bool live = g < n_groups;  // multiple of 4
+  uint4 v = live ? x[g] : make_uint4(0, 0, 0, 0);
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  float f[8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16_to_f32(w[i] & 0xffffu);
+    f[2 * i + 1] = bf16_to_f32(w[i] >> 16);
+    amax = fmaxf(amax, fmaxf(fabsf(f[2 * i]), fabsf(f[2 * i + 1])));
+  }
+  amax = wave_max_xor(amax, 4);
+  int k;
+  if (rule == 0) {
+    amax = fmaxf(amax, 6.0f * 1.1754943508222875e-38f);
+    float vs = fmaxf(amax * (1.0f / 6.0f), 1.1754943508222875e-38f);
+    k = ceil_log2(vs);
+  } else {
+    k = (amax == 0.0f) ? -127 : min(max(floor_log2(amax) - 2, -127), 127);
+  }
+  float s = pow2f(k), inv = pow2f(-k);
+  uint32_t pk = 0;
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    float y = f[i] * inv;
+    uint32_t neg;
+    float a;
+    if (rule == 0) {
+      y = fminf(fmaxf(y, -6.0f), 6.0f);
+      neg = (y < 0.0f) ? 1u : 0u;
+      a = fabsf(y);
+    } else {
+      neg = __float_as_uint(f[i]) >> 31;
+      a = fminf(fabsf(y), 6.0f);
+    }
+    uint32_t mag = e2m1_mag_code(a);
+    pk |= (mag | (neg << 3)) << (4 * i);
+    float q = e2m1_mag_value(mag) * s;
+    uint32_t b = f32_to_bf16(neg ? -q : q);
+    if (i & 1) o[i >> 1] |= b << 16; else o[i >> 1] = b;
+  }
+  if (!live) return;
+  packed[g] = pk;
+  if (dq) dq[g] = make_uint4(o[0], o[1], o[2], o[3]);
+  if ((threadIdx.x & 3) == 0) scale[g >> 2] = (uint8_t)(k + 127);
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+hipError_t launch_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, uint16_t* out,
+                                int64_t n_elems, hipStream_t st) {
+  int64_t n_groups = n_elems / 8;
+  if (n_groups == 0) return hipSuccess;
+  int64_t want = (n_groups + 255) / 256;
+  int grid = (int)(want < 8192 ? want : 8192);
+  hipLaunchKernelGGL(mxfp4_dequant_kernel, dim3(grid), dim3(256), 0, st,
+                     (const uint32_t*)packed, scales, (u32x4*)out, n_groups);
+  return hipGetLastError();
+}
+
+hipError_t launch_fp8_act_quant(const uint16_t* x, int64_t n_elems, uint16_t* rt, uint8_t* codes,
+                                float* scale_f32, uint8_t* scale_e8m0x4, hipStream_t st) {
+  int64_t n_groups = n_elems / 8;
+  if (n_groups == 0) return hipSuccess;
+  int grid = (int)((n_groups + 255) / 256);
+  hipLaunchKernelGGL(fp8_act_quant_kernel, dim3(grid), dim3(256), 0, st, (const uint4*)x, n_groups,
+                     (uint4*)rt, (uint2*)codes, scale_f32, (uint32_t*)scale_e8m0x4);
+  return hipGetLastError();
+}
+
+hipError_t launch_mxfp4_act_quant(const uint16_t* x, int64_t n_elems, int rule, uint8_t* packed,
+                                  uint8_t* scale, uint16_t* dq, hipStream_t st) {
+  int64_t n_groups = n_elems / 8;
+  if (n_groups == 0) return hipSuccess;
+  int grid = (int)((n_groups + 255) / 256);
+  hipLaunchKernelGGL(mxfp4_act_quant_kernel, dim3(grid), dim3(256), 0, st, (const uint4*)x, n_groups,
+                     rule, (uint32_t*)packed, scale, (uint4*)dq);
+  return hipGetLastError();
+}

@@ -1,0 +1,88 @@
+"""ctypes binding of ``libdsv4hip.so`` (the C ABI declared in ``include/dsv4_moe.h``).
+
+The library is built in-tree (``make -C csrc``, driven by ``__graft_entry__.build``)
+and loaded from this directory. There is no fallback: if the library is
+missing or fails to load, every call raises.
+"""
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libdsv4hip.so")
+
+DSV4_OK = 0
+AFMT_E4M3 = 0
+AFMT_E2M1 = 1
+PROFILE_BF16 = 0
+PROFILE_A4W4 = 1
+RULE_CEIL_DIV6 = 0
+RULE_OCP_FLOOR = 1
+GEMM_BLOCK_M = 16
+MAX_EXPERTS = 512
+MAX_TOPK = 32
+
+_c_p = ctypes.c_void_p
+_i32 = ctypes.c_int
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "dsv4_last_error": (ctypes.c_char_p, []),
+    "dsv4_abi_version": (_i32, []),
+    "dsv4_mxfp4_dequant_bf16": (_i32, [_c_p, _c_p, _c_p, _i64, _i64, _c_p]),
+    "dsv4_fp8_act_quant": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p, _c_p]),
+    "dsv4_mxfp4_act_quant": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p]),
+    "dsv4_moe_align_max_blocks": (_i32, [_i32, _i32, _i32]),
+    "dsv4_moe_align": (_i32, [_c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32] + [_c_p] * 13 + [_c_p]),
+    "dsv4_moe_permute": (_i32, [_c_p, _i64, _c_p, _i64, _i64, _c_p, _c_p]),
+    "dsv4_moe_unpermute_workspace_bytes": (_i64, [_i32, _i32]),
+    "dsv4_moe_unpermute": (_i32, [_c_p, _c_p, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p]),
+    "dsv4_moe_combine": (_i32, [_c_p, _c_p, _i32, _i32, _i32, _i32, _c_p, _c_p]),
+    "dsv4_moe_gemm_gateup": (_i32, [_i32, _c_p, _c_p, _i32, _c_p, _c_p, _c_p, _i32, _i32, _i32, _c_p, _i32,
+                                    _i32, _c_p, _f32, _c_p, _c_p]),
+    "dsv4_moe_gemm_down": (_i32, [_i32, _c_p, _c_p, _c_p, _c_p, _c_p, _i32, _i32, _i32, _c_p, _i32, _i32,
+                                  _c_p, _c_p]),
+    "dsv4_moe_layer_workspace_bytes": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i64)]),
+    "dsv4_moe_layer_forward": (_i32, [_i32, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32, _c_p,
+                                      _f32, _c_p, _i64, _c_p, _c_p]),
+}
+
+_LIB = None
+
+
+class Dsv4Error(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+    def __init__(self, fn, code, msg):
+        super().__init__(f"{fn} failed ({code}): {msg}")
+        self.code = code
+
+
+def lib():
+    """Load (once) and return the HIP library; raises if it is not built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run __graft_entry__.build() (or make -C csrc). "
+                "The MoE expert path has no implementation other than this HIP library.")
+        h = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        if h.dsv4_abi_version() != 1:
+            raise RuntimeError("libdsv4hip.so ABI version mismatch")
+        _LIB = h
+    return _LIB
+
+
+def call(name, *args):
+    """Call a status-returning entry point and raise ``Dsv4Error`` on failure."""
+    rc = getattr(lib(), name)(*args)
+    if rc != DSV4_OK:
+        msg = lib().dsv4_last_error().decode(errors="replace")
+        raise Dsv4Error(name, rc, msg)
+    return rc

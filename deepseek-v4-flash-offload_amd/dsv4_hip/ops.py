@@ -1,0 +1,299 @@
+"""torch-facing wrappers of the HIP kernels.
+
+Tensors must live on a ROCm device; outputs are allocated with torch on the
+input's device and every kernel is enqueued on torch's current stream for that
+device. There is no CPU implementation: a CPU tensor raises.
+"""
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import call
+
+_E8M0 = getattr(torch, "float8_e8m0fnu", None)
+
+
+def _dev(t: torch.Tensor, what: str) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{what}: expected a torch.Tensor, got {type(t).__name__}")
+    if not t.is_cuda:
+        raise RuntimeError(f"{what}: the HIP MoE path needs a ROCm device tensor (got {t.device}); "
+                           "there is no CPU implementation")
+    return t
+
+
+def _u8(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype in (torch.uint8, torch.int8) or (_E8M0 is not None and t.dtype == _E8M0):
+        return t.contiguous().view(torch.uint8)
+    raise TypeError(f"expected a byte tensor (uint8/int8/e8m0), got {t.dtype}")
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+# ---------------------------------------------------------------------------
+# dequant / quant
+# ---------------------------------------------------------------------------
+def dequant_mxfp4(w_packed: torch.Tensor, scale: torch.Tensor, out: Optional[torch.Tensor] = None):
+    """[N, K/2] packed + [N, K/32] E8M0 -> bf16 [N, K] (bit-exact)."""
+    _dev(w_packed, "dequant_mxfp4")
+    wp, sc = _u8(w_packed), _u8(scale)
+    if wp.dim() != 2 or sc.dim() != 2:
+        raise ValueError("dequant_mxfp4 expects 2-D packed and scale tensors")
+    N, K2 = wp.shape
+    K = 2 * K2
+    if sc.shape != (N, K // 32):
+        raise ValueError(f"scale shape {tuple(sc.shape)} does not match packed {tuple(wp.shape)}")
+    if out is None:
+        out = torch.empty((N, K), dtype=torch.bfloat16, device=wp.device)
+    call("dsv4_mxfp4_dequant_bf16", _p(wp), _p(sc), _p(out), N, K, _stream(wp))
+    return out
+
+
+def fp8_act_quant(x: torch.Tensor, block_size: int = 128, rt: Optional[torch.Tensor] = None,
+                  want_codes: bool = False, want_scale: bool = False, want_e8m0x4: bool = False):
+    """Per-128 FP8 E4M3 quantisation of a bf16 tensor (last dim blocked).
+
+    Returns a dict with the requested outputs: ``rt`` (bf16 round trip, may be
+    ``x`` itself for the inplace form), ``codes`` (uint8), ``scale`` (fp32 per
+    block) and ``e8m0x4`` (uint8 per 32 elements)."""
+    _dev(x, "fp8_act_quant")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"fp8_act_quant: bf16 input required, got {x.dtype}")
+    if not x.is_contiguous():
+        raise ValueError("fp8_act_quant: input must be contiguous")
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    res = {}
+    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device) if want_codes else None
+    scale = torch.empty((*x.shape[:-1], cols // block_size), dtype=torch.float32,
+                        device=x.device) if want_scale else None
+    e8 = torch.empty((*x.shape[:-1], cols // 32), dtype=torch.uint8, device=x.device) if want_e8m0x4 else None
+    call("dsv4_fp8_act_quant", _p(x), rows, cols, block_size, _p(rt), _p(codes), _p(scale), _p(e8), _stream(x))
+    if rt is not None:
+        res["rt"] = rt
+    if codes is not None:
+        res["codes"] = codes
+    if scale is not None:
+        res["scale"] = scale
+    if e8 is not None:
+        res["e8m0x4"] = e8
+    return res
+
+
+def mxfp4_act_quant(x: torch.Tensor, rule: int, dq: Optional[torch.Tensor] = None, want_packed: bool = True):
+    """Per-32 MXFP4 quantisation. Returns (packed uint8 [.., K/2], scale uint8 [.., K/32], dq)."""
+    _dev(x, "mxfp4_act_quant")
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"mxfp4_act_quant: bf16 input required, got {x.dtype}")
+    if not x.is_contiguous():
+        raise ValueError("mxfp4_act_quant: input must be contiguous")
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    packed = torch.empty((*x.shape[:-1], cols // 2), dtype=torch.uint8, device=x.device)
+    scale = torch.empty((*x.shape[:-1], cols // 32), dtype=torch.uint8, device=x.device)
+    call("dsv4_mxfp4_act_quant", _p(x), rows, cols, int(rule), _p(packed), _p(scale), _p(dq), _stream(x))
+    return packed, scale, dq
+
+
+# ---------------------------------------------------------------------------
+# routing layout
+# ---------------------------------------------------------------------------
+@dataclass
+class AlignResult:
+    """Device tensors of one moe_align call (all int32 unless noted)."""
+    T: int
+    K: int
+    E: int
+    block_m: int
+    max_blocks: int
+    sorted_ids: torch.Tensor
+    block_expert: torch.Tensor
+    num_post_padded: torch.Tensor
+    order: torch.Tensor
+    s_e: torch.Tensor
+    s_w: torch.Tensor          # fp32
+    row: torch.Tensor
+    counts: torch.Tensor
+    expert_start: torch.Tensor
+    active: torch.Tensor       # [E], ascending active ids then -1
+    num_active: torch.Tensor
+    padded_pos: torch.Tensor
+    status: torch.Tensor
+
+    def check(self):
+        """Host-synchronising check of the kernel's status word."""
+        s = int(self.status.item())
+        if s & (1 << 30):
+            raise RuntimeError("moe_align: max_blocks too small")
+        if s:
+            raise ValueError(f"moe_align: {s} expert id(s) outside [0, {self.E})")
+
+    def active_list(self) -> torch.Tensor:
+        """``active`` trimmed to its length (host sync)."""
+        return self.active[: int(self.num_active.item())]
+
+
+def max_blocks(R: int, E: int, block_m: int) -> int:
+    return int(_lib.lib().dsv4_moe_align_max_blocks(R, E, block_m))
+
+
+def moe_align(topk_ids: torch.Tensor, topk_w: Optional[torch.Tensor], n_experts: int,
+              block_m: int = _lib.GEMM_BLOCK_M) -> AlignResult:
+    _dev(topk_ids, "moe_align")
+    if topk_ids.dim() != 2:
+        raise ValueError("moe_align expects topk_ids of shape [T, K]")
+    if topk_ids.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"moe_align: int32/int64 ids required, got {topk_ids.dtype}")
+    ids = topk_ids.contiguous()
+    T, K = ids.shape
+    R = T * K
+    dev = ids.device
+    w = None
+    if topk_w is not None:
+        w = topk_w.to(torch.float32).contiguous()
+        if w.shape != ids.shape:
+            raise ValueError("moe_align: topk_w shape must match topk_ids")
+    mb = max_blocks(R, n_experts, block_m)
+    i32 = dict(dtype=torch.int32, device=dev)
+    res = AlignResult(
+        T=T, K=K, E=n_experts, block_m=block_m, max_blocks=mb,
+        sorted_ids=torch.empty(mb * block_m, **i32), block_expert=torch.empty(mb, **i32),
+        num_post_padded=torch.empty(1, **i32), order=torch.empty(R, **i32), s_e=torch.empty(R, **i32),
+        s_w=torch.empty(R, dtype=torch.float32, device=dev), row=torch.empty(R, **i32),
+        counts=torch.empty(n_experts, **i32), expert_start=torch.empty(n_experts, **i32),
+        active=torch.empty(n_experts, **i32), num_active=torch.empty(1, **i32),
+        padded_pos=torch.empty(R, **i32), status=torch.empty(1, **i32))
+    call("dsv4_moe_align", _p(ids), 1 if ids.dtype == torch.int64 else 0, _p(w), T, K, n_experts, block_m, mb,
+         _p(res.sorted_ids), _p(res.block_expert), _p(res.num_post_padded), _p(res.order), _p(res.s_e),
+         _p(res.s_w if w is not None else None), _p(res.row), _p(res.counts), _p(res.expert_start),
+         _p(res.active), _p(res.num_active), _p(res.padded_pos), _p(res.status), _stream(ids))
+    if w is None:
+        res.s_w.zero_()
+    return res
+
+
+def moe_permute(x: torch.Tensor, row: torch.Tensor) -> torch.Tensor:
+    """``x[row]`` for row-major x whose rows are a multiple of 16 bytes."""
+    _dev(x, "moe_permute")
+    x = x.contiguous()
+    row = row.to(torch.int32).contiguous()
+    n = row.numel()
+    out = torch.empty((n, *x.shape[1:]), dtype=x.dtype, device=x.device)
+    row_bytes = x[0].numel() * x.element_size() if x.shape[0] else 0
+    call("dsv4_moe_permute", _p(x), x.shape[0], _p(row), n, row_bytes, _p(out), _stream(x))
+    return out
+
+
+def moe_unpermute(out_sorted: torch.Tensor, row: torch.Tensor, T: int, kmax: Optional[int] = None):
+    """``zeros(T, D).index_add_(0, row, out.float()).bf16()`` (bit-exact)."""
+    _dev(out_sorted, "moe_unpermute")
+    if out_sorted.dtype != torch.bfloat16:
+        raise TypeError("moe_unpermute: bf16 rows required")
+    out_sorted = out_sorted.contiguous()
+    row = row.to(torch.int32).contiguous()
+    R, D = out_sorted.shape
+    if kmax is None:
+        kmax = max(1, -(-R // max(T, 1)))
+    ws = torch.empty(int(_lib.lib().dsv4_moe_unpermute_workspace_bytes(T, kmax)), dtype=torch.uint8,
+                     device=out_sorted.device)
+    y = torch.empty((T, D), dtype=torch.bfloat16, device=out_sorted.device)
+    call("dsv4_moe_unpermute", _p(out_sorted), _p(row), R, T, kmax, D, _p(ws), _p(y), _stream(out_sorted))
+    return y
+
+
+def moe_combine(out_flat: torch.Tensor, topk_ids: torch.Tensor) -> torch.Tensor:
+    """Sum each token's K rows (row t*K+k) in ascending expert order -> bf16 [T, D]."""
+    _dev(out_flat, "moe_combine")
+    ids = topk_ids.contiguous()
+    T, K = ids.shape
+    D = out_flat.shape[-1]
+    y = torch.empty((T, D), dtype=torch.bfloat16, device=out_flat.device)
+    call("dsv4_moe_combine", _p(out_flat.contiguous()), _p(ids), 1 if ids.dtype == torch.int64 else 0, T, K, D,
+         _p(y), _stream(out_flat))
+    return y
+
+
+# ---------------------------------------------------------------------------
+# expert table + GEMMs + fused layer
+# ---------------------------------------------------------------------------
+_KEYS = ("w1p", "w1s", "w2p", "w2s", "w3p", "w3s")
+
+
+def expert_table(experts, n_experts: int, device) -> torch.Tensor:
+    """Device table [E, 6] (uint64 as int64) of the packed weight pointers.
+
+    ``experts`` maps expert id -> dict with keys ``w{1,2,3}{p,s}`` (device
+    tensors, contiguous, any byte dtype). Missing experts get null entries."""
+    tab = torch.zeros((n_experts, 6), dtype=torch.int64)
+    items = experts.items() if hasattr(experts, "items") else enumerate(experts)
+    for e, d in items:
+        if d is None:
+            continue
+        for j, k in enumerate(_KEYS):
+            t = d[k]
+            _dev(t, "expert_table")
+            if not t.is_contiguous():
+                raise ValueError(f"expert {e} {k}: weights must be contiguous")
+            if t.data_ptr() % 16:
+                raise ValueError(f"expert {e} {k}: weights must be 16-byte aligned")
+            tab[int(e), j] = t.data_ptr()
+    return tab.to(device)
+
+
+def gemm_gateup(afmt, a, a_scale, a_row_div, al: AlignResult, table, D, I, topk_w_flat, swiglu_limit):
+    R = al.T * al.K
+    h = torch.empty((R, I), dtype=torch.bfloat16, device=a.device)
+    call("dsv4_moe_gemm_gateup", afmt, _p(a), _p(a_scale), a_row_div, _p(al.sorted_ids), _p(al.block_expert),
+         _p(al.num_post_padded), R, al.block_m, al.max_blocks, _p(table), D, I, _p(topk_w_flat),
+         float(swiglu_limit or 0.0), _p(h), _stream(a))
+    return h
+
+
+def gemm_down(afmt, a, a_scale, al: AlignResult, table, I, D):
+    R = al.T * al.K
+    out = torch.empty((R, D), dtype=torch.bfloat16, device=a.device)
+    call("dsv4_moe_gemm_down", afmt, _p(a), _p(a_scale), _p(al.sorted_ids), _p(al.block_expert),
+         _p(al.num_post_padded), R, al.block_m, al.max_blocks, _p(table), I, D, _p(out), _stream(a))
+    return out
+
+
+class LayerRunner:
+    """Holds a reusable workspace for ``dsv4_moe_layer_forward`` (one routed layer)."""
+
+    def __init__(self, device, n_experts: int, hidden: int, inter: int):
+        self.device = torch.device(device)
+        self.E, self.D, self.I = n_experts, hidden, inter
+        self._ws = None
+
+    def workspace(self, T, K, profile):
+        n = ctypes.c_int64(0)
+        call("dsv4_moe_layer_workspace_bytes", T, K, self.E, self.D, self.I, profile, ctypes.byref(n))
+        if self._ws is None or self._ws.numel() < n.value:
+            self._ws = torch.empty(max(n.value, 256), dtype=torch.uint8, device=self.device)
+        return self._ws
+
+    def forward(self, x, topk_ids, topk_w, table, profile=_lib.PROFILE_BF16, rule=_lib.RULE_OCP_FLOOR,
+                swiglu_limit=10.0, out=None):
+        _dev(x, "layer_forward")
+        if x.dtype != torch.bfloat16 or not x.is_contiguous():
+            raise TypeError("layer_forward: contiguous bf16 activations required")
+        T, D = x.shape
+        ids = topk_ids.contiguous()
+        K = ids.shape[1]
+        w = topk_w.to(torch.float32).contiguous()
+        ws = self.workspace(T, K, profile)
+        y = out if out is not None else torch.empty((T, D), dtype=torch.bfloat16, device=x.device)
+        call("dsv4_moe_layer_forward", profile, rule, _p(x), _p(ids), 1 if ids.dtype == torch.int64 else 0,
+             _p(w), T, K, self.E, D, self.I, _p(table), float(swiglu_limit or 0.0), _p(ws), ws.numel(), _p(y),
+             _stream(x))
+        return y

@@ -1,0 +1,158 @@
+/* C ABI of libdsv4hip.so - the MI355X (gfx950) routed-MoE expert path.
+ *
+ * Drop-in boundary for the expert hot path of the DeepSeek-V4 offload plugin.
+ * Each entry point names the reference interface it replaces (file:line in the
+ * reference repository). Conventions:
+ *   - every pointer argument is a device pointer unless stated otherwise;
+ *     buffers are owned by the caller (no allocation, no synchronisation);
+ *   - `stream` is a hipStream_t passed as void* (NULL = default stream);
+ *   - bf16 tensors are 16-bit patterns, row-major, contiguous;
+ *   - MXFP4 tensors are the checkpoint layout: [N, K/2] bytes (two E2M1
+ *     nibbles per byte, low nibble = even k) plus [N, K/32] E8M0 bytes;
+ *   - return value: DSV4_OK (0) or a negative DSV4_ERR_* code, with a message
+ *     available from dsv4_last_error() (thread-local).
+ */
+#ifndef DSV4_MOE_H
+#define DSV4_MOE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DSV4_ABI_VERSION 1
+
+#define DSV4_MAX_EXPERTS 512
+#define DSV4_MAX_TOPK 32
+#define DSV4_GEMM_BLOCK_M 16
+
+/* activation formats of the grouped GEMM A operand */
+#define DSV4_AFMT_E4M3 0 /* one E4M3fn code per byte, E8M0 per 32 (bf16 profile) */
+#define DSV4_AFMT_E2M1 1 /* two E2M1 codes per byte, E8M0 per 32 (a4w4 profile) */
+
+/* profiles of the routed layer */
+#define DSV4_PROFILE_BF16 0 /* deepseek_v4.py:166-197 (FP8 round-trip activations) */
+#define DSV4_PROFILE_A4W4 1 /* deepseek_v4.py:199-245 (MXFP4 activations)          */
+
+/* MXFP4 activation scale rules */
+#define DSV4_RULE_CEIL_DIV6 0 /* 2^ceil(log2(amax/6)), npu_ops.py:107-121 */
+#define DSV4_RULE_OCP_FLOOR 1 /* 2^(floor(log2 amax)-2), OCP MX v1.0      */
+
+/* status codes (csrc/common.h) */
+#define DSV4_OK 0
+#define DSV4_ERR_NULL (-1)
+#define DSV4_ERR_SHAPE (-2)
+#define DSV4_ERR_UNSUPPORTED (-3)
+#define DSV4_ERR_HIP (-4)
+#define DSV4_ERR_STATE (-5)
+
+/* Per-expert weight pointers read by the grouped GEMMs (device array indexed
+ * by expert id, 48 bytes per entry). Entries of experts that no token routes
+ * to are never read. */
+typedef struct {
+  const void* w1p; const void* w1s; /* gate  [I, D/2] + [I, D/32] */
+  const void* w2p; const void* w2s; /* down  [D, I/2] + [D, I/32] */
+  const void* w3p; const void* w3s; /* up    [I, D/2] + [I, D/32] */
+} dsv4_expert_ptrs;
+
+const char* dsv4_last_error(void);
+int dsv4_abi_version(void);
+
+/* MXFP4 weight -> bf16, bit-exact with the reference's torch math.
+ * Replaces npu_ops.dequant_fp4_weight (npu_ops.py:142-158).
+ * packed [n_rows, k/2], scales [n_rows, k/32], out [n_rows, k]; k % 32 == 0. */
+int dsv4_mxfp4_dequant_bf16(const void* packed, const void* scales, void* out, int64_t n_rows, int64_t k,
+                            void* stream);
+
+/* Per-128 FP8 E4M3 activation quantisation with power-of-two scales.
+ * Replaces npu_ops.act_quant (npu_ops.py:73-104): `rt` receives the inplace
+ * round trip (what act_quant(x, 128, "ue8m0", None, True) writes), `codes` the
+ * E4M3fn bytes, `scale_f32` the fp32 scale per block ([rows, cols/128]) and
+ * `scale_e8m0x4` the E8M0 byte of the block repeated for each 32 elements
+ * ([rows, cols/32]). Any output may be NULL (at least one must not be). */
+int dsv4_fp8_act_quant(const void* x, int64_t rows, int64_t cols, int block_size, void* rt, void* codes,
+                       void* scale_f32, void* scale_e8m0x4, void* stream);
+
+/* Per-32 MXFP4 activation quantisation: packed [rows, cols/2], E8M0 scale
+ * [rows, cols/32], optional bf16 dequantised view `dq` [rows, cols].
+ * rule DSV4_RULE_CEIL_DIV6 replaces npu_ops.fp4_act_quant (npu_ops.py:107-121;
+ * `dq` is its inplace result); rule DSV4_RULE_OCP_FLOOR replaces the call sites
+ * of torch_npu.npu_dynamic_mx_quant (deepseek_v4.py:212, 240). */
+int dsv4_mxfp4_act_quant(const void* x, int64_t rows, int64_t cols, int rule, void* packed, void* scale, void* dq,
+                         void* stream);
+
+/* Upper bound of padded M blocks for R routed entries (host function). */
+int dsv4_moe_align_max_blocks(int R, int E, int block_m);
+
+/* Stable sort of the T*K routed entries by expert, with counts and the padded
+ * block layout. Replaces the inline sort/count of deepseek_v4.py:155-164
+ * (flat_e, argsort -> order, s_e, s_w, row = order // K, bincount -> counts,
+ * nonzero -> active). Order is (expert asc, flat index asc) = argsort(stable).
+ * topk_ids: [T, K] int32 or int64 (ids_int64 = 1). topk_w: [T, K] fp32 or NULL.
+ * Required outputs: sorted_ids [max_blocks*block_m] (flat index t*K+k of each
+ * padded slot, T*K marks padding), block_expert [max_blocks], num_post_padded
+ * [1]. Optional (NULL to skip): order, s_e, s_w, row [T*K]; counts,
+ * expert_start (first padded slot), active (ascending, -1 tail) [E];
+ * num_active [1]; padded_pos [T*K] (padded slot of each flat index); status
+ * [1] (number of out-of-range ids, plus 2^30 if max_blocks was too small). */
+int dsv4_moe_align(const void* topk_ids, int ids_int64, const float* topk_w, int T, int K, int E, int block_m,
+                   int max_blocks, int32_t* sorted_ids, int32_t* block_expert, int32_t* num_post_padded,
+                   int32_t* order, int32_t* s_e, float* s_w, int32_t* row, int32_t* counts, int32_t* expert_start,
+                   int32_t* active, int32_t* num_active, int32_t* padded_pos, int32_t* status, void* stream);
+
+/* dst[i] = src[row[i]] for rows of row_bytes bytes (multiple of 16); src has
+ * n_src rows and a row index outside [0, n_src) yields a zero row.
+ * Replaces the gathers x_sorted = xq[row] (deepseek_v4.py:171, 213-214). */
+int dsv4_moe_permute(const void* src, int64_t n_src, const int32_t* row, int64_t n_rows, int64_t row_bytes,
+                     void* dst, void* stream);
+
+/* y = bf16(zeros(T, D) fp32 .index_add_(0, row, out_sorted.float())), summed in
+ * ascending sorted position per token, bit-exact. Replaces
+ * deepseek_v4.py:195-197 / 243-245. Each token may appear at most Kmax times.
+ * workspace: dsv4_moe_unpermute_workspace_bytes(T, Kmax) bytes of device memory. */
+int64_t dsv4_moe_unpermute_workspace_bytes(int T, int Kmax);
+int dsv4_moe_unpermute(const void* out_sorted, const int32_t* row, int R, int T, int Kmax, int D, void* workspace,
+                       void* y, void* stream);
+
+/* Same combine for rows stored by flat index (row t*K+k = the k-th pick of
+ * token t): each token's rows are summed in ascending expert id, which is the
+ * order index_add_ visits them in. Used by the fused layer. */
+int dsv4_moe_combine(const void* out_flat, const void* topk_ids, int ids_int64, int T, int K, int D, void* y,
+                     void* stream);
+
+/* Grouped gate/up GEMM over all routed rows in one launch, fused with the
+ * SwiGLU epilogue of deepseek_v4.py:184-187: h[f] = silu(min(g,L)) *
+ * clamp(u,-L,L) * topk_w[f] where g/u are the bf16-rounded GEMM outputs.
+ * Replaces the two npu_grouped_matmul calls of deepseek_v4.py:177-182
+ * (afmt E4M3) / 231-232 (afmt E2M1). A rows are gathered on load: padded slot
+ * p reads A row sorted_ids[p] / a_row_div. a: [rows, D] codes (E4M3) or
+ * [rows, D/2] (E2M1), a_scale [rows, D/32]. h_out: bf16 [R, I] by flat index. */
+int dsv4_moe_gemm_gateup(int afmt, const void* a, const void* a_scale, int a_row_div, const int32_t* sorted_ids,
+                         const int32_t* block_expert, const int32_t* num_post_padded, int R, int block_m,
+                         int max_blocks, const void* expert_table, int D, int I, const float* topk_w,
+                         float swiglu_limit, void* h_out, void* stream);
+
+/* Grouped down GEMM: out[f] = bf16(a[f] @ W2[e]^T) for every routed row.
+ * Replaces npu_grouped_matmul of deepseek_v4.py:190-193 / 241.
+ * a: [R, I] (E4M3) or [R, I/2] (E2M1) by flat index, a_scale [R, I/32]. */
+int dsv4_moe_gemm_down(int afmt, const void* a, const void* a_scale, const int32_t* sorted_ids,
+                       const int32_t* block_expert, const int32_t* num_post_padded, int R, int block_m,
+                       int max_blocks, const void* expert_table, int I, int D, void* out, void* stream);
+
+/* The whole routed expert computation of one layer, i.e. the body of
+ * OffloadDeepseekV4MoE._routed (deepseek_v4.py:150-197, profile BF16) or
+ * _routed_mxfp4 (deepseek_v4.py:199-245, profile A4W4) after routing:
+ * moe_align -> activation quant -> gate/up GEMM + SwiGLU -> h quant -> down
+ * GEMM -> combine. x [T, D] bf16, topk_ids/topk_w [T, K], y [T, D] bf16.
+ * scale_rule applies to the A4W4 profile only. */
+int dsv4_moe_layer_workspace_bytes(int T, int K, int E, int D, int I, int profile, int64_t* bytes);
+int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
+                           const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
+                           float swiglu_limit, void* workspace, int64_t workspace_bytes, void* y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSV4_MOE_H */

@@ -1,0 +1,156 @@
+"""GPU parity of the grouped GEMMs and the fused routed layer.
+
+Tolerance: normwise max relative error
+    rel = max|gpu - oracle| / max|oracle|
+<= 1e-2 for the bf16 profile and <= 2e-2 for the a4w4 profile. Stage tests
+feed the GPU kernel and the oracle the *same* quantised operands, so the only
+difference is fp32 summation order (and the bf16 roundings that follow it);
+the end-to-end tests start from the same bf16 x and routing.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mxfp4 as Q
+from oracle import moe as M
+from dsv4_hip import ops, synth, AFMT_E2M1, AFMT_E4M3, PROFILE_A4W4, PROFILE_BF16, RULE_OCP_FLOOR, RULE_CEIL_DIV6
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"bf16": 1e-2, "a4w4": 2e-2}
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def _bits(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _dev_bf16(bits, dev):
+    return torch.from_numpy(np.ascontiguousarray(bits, np.uint16).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def _dev(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def make_layer(E, D, I, experts_needed, dev):
+    host = {e: synth.expert_weights(int(e), D, I) for e in experts_needed}
+    devw = {e: {k: _dev(v, dev) for k, v in d.items()} for e, d in host.items()}
+    return host, devw, ops.expert_table(devw, E, dev)
+
+
+def _case(T, K, E, D, I, seed, dev):
+    ids = synth.zipf_topk(T, K, E, synth.rank_permutation(E, 3), np.random.default_rng(seed))
+    w = synth.routing_weights(T, K, seed + 1)
+    x = synth.bf16_normal(np.random.default_rng(seed + 2), (T, D))
+    xb = x.view(torch.int16).numpy().view(np.uint16)
+    host, devw, table = make_layer(E, D, I, np.unique(ids), dev)
+    return ids, w, xb, host, devw, table
+
+
+@pytest.mark.parametrize("profile", ["bf16", "a4w4"])
+@pytest.mark.parametrize("T,K,E,D,I", [(24, 4, 16, 1024, 512), (200, 8, 16, 512, 512), (8, 8, 256, 4096, 2048)])
+def test_grouped_gemm_stages(gpu, profile, T, K, E, D, I):
+    ids, w, xb, host, devw, table = _case(T, K, E, D, I, 31 + T, gpu)
+    al = ops.moe_align(_dev(ids, gpu), _dev(w, gpu), E, 16)
+    R = T * K
+    if profile == "bf16":
+        rt, codes, s, k = Q.act_quant(xb, 128)
+        a_f = Q.bf16_bits_to_f32(rt)
+        a = _dev(codes, gpu)
+        a_s = _dev(np.repeat((k + 127).astype(np.uint8), 4, axis=-1), gpu)
+        afmt = AFMT_E4M3
+    else:
+        _, packed, sc = Q.ocp_mx_quant(xb, 32)
+        a_f = Q.fp4_codes_to_f32(packed, sc)
+        a, a_s, afmt = _dev(packed, gpu), _dev(sc, gpu), AFMT_E2M1
+    h = ops.gemm_gateup(afmt, a, a_s, K, al, table, D, I, _dev(w.reshape(-1), gpu), 10.0)
+    torch.cuda.synchronize()
+    # oracle gate/up + SwiGLU for each flat row on the same quantised x
+    flat_e = ids.reshape(-1)
+    h_ref = np.zeros((R, I), np.float32)
+    for e in np.unique(flat_e):
+        rows = np.nonzero(flat_e == e)[0]
+        w1 = Q.dequant_fp4_weight_f32(host[e]["w1p"], host[e]["w1s"])
+        w3 = Q.dequant_fp4_weight_f32(host[e]["w3p"], host[e]["w3s"])
+        xa = a_f[rows // K]
+        g = Q.f32_to_bf16_f32(M.matmul_nt(xa, w1))
+        u = Q.f32_to_bf16_f32(M.matmul_nt(xa, w3))
+        h_ref[rows] = M.swiglu(g, u, w.reshape(-1)[rows], 10.0)
+    h_gpu = Q.bf16_bits_to_f32(_bits(h))
+    assert rel(h_gpu, Q.f32_to_bf16_f32(h_ref)) <= TOL[profile]
+    # down GEMM on the oracle's quantised h
+    hb = Q.f32_to_bf16_bits(h_ref)
+    if profile == "bf16":
+        hrt, hc, hs, hk = Q.act_quant(hb, 128)
+        ha_f = Q.bf16_bits_to_f32(hrt)
+        ha, has = _dev(hc, gpu), _dev(np.repeat((hk + 127).astype(np.uint8), 4, axis=-1), gpu)
+    else:
+        _, hp, hsc = Q.ocp_mx_quant(hb, 32)
+        ha_f = Q.fp4_codes_to_f32(hp, hsc)
+        ha, has = _dev(hp, gpu), _dev(hsc, gpu)
+    out = ops.gemm_down(afmt, ha, has, al, table, I, D)
+    torch.cuda.synchronize()
+    out_ref = np.zeros((R, D), np.float32)
+    for e in np.unique(flat_e):
+        rows = np.nonzero(flat_e == e)[0]
+        w2 = Q.dequant_fp4_weight_f32(host[e]["w2p"], host[e]["w2s"])
+        out_ref[rows] = M.matmul_nt(ha_f[rows], w2)
+    assert rel(Q.bf16_bits_to_f32(_bits(out)), Q.f32_to_bf16_f32(out_ref)) <= TOL[profile]
+
+
+def test_grouped_gemm_empty_group_pattern(gpu):
+    # _bench_gmm.py:8-22: groups [2, 0, 3] -> expert 1 receives no rows
+    E, D, I, K = 3, 512, 512, 1
+    ids = np.array([[0], [0], [2], [2], [2]], np.int64)
+    w = np.ones((5, 1), np.float32)
+    xb = synth.bf16_normal(np.random.default_rng(0), (5, D)).view(torch.int16).numpy().view(np.uint16)
+    host, devw, table = make_layer(E, D, I, [0, 2], gpu)
+    al = ops.moe_align(_dev(ids, gpu), _dev(w, gpu), E, 16)
+    rt, codes, s, k = Q.act_quant(xb, 128)
+    h = ops.gemm_gateup(AFMT_E4M3, _dev(codes, gpu), _dev(np.repeat((k + 127).astype(np.uint8), 4, -1), gpu), K,
+                        al, table, D, I, _dev(w.reshape(-1), gpu), 10.0)
+    torch.cuda.synchronize()
+    a_f = Q.bf16_bits_to_f32(rt)
+    for e, rows in ((0, [0, 1]), (2, [2, 3, 4])):
+        w1 = Q.dequant_fp4_weight_f32(host[e]["w1p"], host[e]["w1s"])
+        w3 = Q.dequant_fp4_weight_f32(host[e]["w3p"], host[e]["w3s"])
+        g = Q.f32_to_bf16_f32(M.matmul_nt(a_f[rows], w1))
+        u = Q.f32_to_bf16_f32(M.matmul_nt(a_f[rows], w3))
+        ref = M.swiglu(g, u, np.ones(len(rows), np.float32), 10.0)
+        assert rel(Q.bf16_bits_to_f32(_bits(h))[rows], ref) <= 1e-2
+
+
+@pytest.mark.parametrize("profile", ["bf16", "a4w4"])
+@pytest.mark.parametrize("T,K,E,D,I", [(8, 8, 256, 4096, 2048), (64, 6, 32, 1024, 512)])
+def test_layer_forward_vs_oracle(gpu, profile, T, K, E, D, I):
+    ids, w, xb, host, devw, table = _case(T, K, E, D, I, 77 + T, gpu)
+    runner = ops.LayerRunner(gpu, E, D, I)
+    x = _dev_bf16(xb, gpu)
+    prof = PROFILE_BF16 if profile == "bf16" else PROFILE_A4W4
+    y = runner.forward(x, _dev(ids, gpu), _dev(w, gpu), table, profile=prof, rule=RULE_OCP_FLOOR)
+    torch.cuda.synchronize()
+    if profile == "bf16":
+        ref = M.routed_bf16(xb, ids, w, host, n_experts=E)
+    else:
+        ref = M.routed_a4w4(xb, ids, w, host, n_experts=E, rule="ocp_floor")
+    got = Q.bf16_bits_to_f32(_bits(y))
+    want = Q.bf16_bits_to_f32(ref["y"])
+    assert rel(got, want) <= TOL[profile], rel(got, want)
+
+
+def test_layer_forward_ceil_rule_and_int32_ids(gpu):
+    T, K, E, D, I = 16, 4, 16, 512, 512
+    ids, w, xb, host, devw, table = _case(T, K, E, D, I, 5, gpu)
+    runner = ops.LayerRunner(gpu, E, D, I)
+    y = runner.forward(_dev_bf16(xb, gpu), _dev(ids.astype(np.int32), gpu), _dev(w, gpu), table,
+                       profile=PROFILE_A4W4, rule=RULE_CEIL_DIV6)
+    torch.cuda.synchronize()
+    ref = M.routed_a4w4(xb, ids, w, host, n_experts=E, rule="ceil_div6")
+    assert rel(Q.bf16_bits_to_f32(_bits(y)), Q.bf16_bits_to_f32(ref["y"])) <= TOL["a4w4"]

@@ -1,0 +1,116 @@
+"""GPU parity: MXFP4 dequant, FP8 act_quant round trip and MXFP4 activation quant.
+
+All bit-exact against the oracle (NaN only arises from E8M0 byte 255 and is
+emitted as 0x7FC0 by both)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import mxfp4 as Q
+from dsv4_hip import ops, synth, RULE_CEIL_DIV6, RULE_OCP_FLOOR
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _bf16_dev(bits, dev):
+    return torch.from_numpy(np.ascontiguousarray(bits, dtype=np.uint16).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def _u8(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint8)).to(dev)
+
+
+def test_dequant_config0_bitexact(gpu):
+    packed, scales, _ = synth.dequant_config0()
+    out = ops.dequant_mxfp4(_u8(packed, gpu), _u8(scales, gpu))
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(out), Q.dequant_fp4_weight(packed, scales))
+
+
+def test_dequant_exhaustive_byte_scale_table(gpu):
+    b = np.tile(np.arange(256, dtype=np.uint8), (256, 16))
+    s = np.repeat(np.arange(256, dtype=np.uint8)[:, None], 256, axis=1)
+    out = ops.dequant_mxfp4(_u8(b, gpu), _u8(s, gpu))
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(out), Q.dequant_fp4_weight(b, s))
+
+
+@pytest.mark.parametrize("n,k", [(1, 32), (3, 96), (4096, 2048), (257, 4096)])
+def test_dequant_shapes_and_tails(gpu, n, k):
+    rng = np.random.default_rng(n + k)
+    packed = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scales = rng.integers(0, 256, (n, k // 32), dtype=np.uint8)
+    out = ops.dequant_mxfp4(_u8(packed, gpu).view(torch.int8), _u8(scales, gpu))
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(out), Q.dequant_fp4_weight(packed, scales))
+
+
+def _all_finite_bf16_rows(cols):
+    b = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    v = Q.bf16_bits_to_f32(b)
+    b = np.where(np.isfinite(v), b, 0).astype(np.uint16)
+    return b.reshape(-1, cols)
+
+
+def test_fp8_act_quant_all_bf16_patterns(gpu):
+    for cols in (128, 4096):
+        xb = _all_finite_bf16_rows(cols)
+        rt, codes, s, k = Q.act_quant(xb, 128)
+        x = _bf16_dev(xb, gpu)
+        r = ops.fp8_act_quant(x, 128, rt=torch.empty_like(x), want_codes=True, want_scale=True, want_e8m0x4=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(_bits(r["rt"]), rt)
+        assert np.array_equal(r["codes"].cpu().numpy(), codes)
+        assert np.array_equal(r["scale"].cpu().numpy(), s)
+        assert np.array_equal(r["e8m0x4"].cpu().numpy(), np.repeat((k + 127).astype(np.uint8), 4, axis=-1))
+
+
+@pytest.mark.parametrize("scale", [1.0, 3.0, 1e-3, 1e-7, 1e4, 3e37])
+def test_fp8_act_quant_random_and_inplace(gpu, scale):
+    rng = np.random.default_rng(int(abs(np.log(scale))) + 1)
+    xf = (rng.standard_normal((64, 512)) * scale).astype(np.float32)
+    xb = Q.f32_to_bf16_bits(xf)
+    rt = Q.act_quant(xb, 128)[0]
+    x = _bf16_dev(xb, gpu)
+    ops.fp8_act_quant(x, 128, rt=x)   # inplace: rt aliases x
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(x), rt)
+
+
+@pytest.mark.parametrize("rule,name", [(RULE_CEIL_DIV6, "ceil_div6"), (RULE_OCP_FLOOR, "ocp_floor")])
+def test_mxfp4_quant_all_bf16_patterns(gpu, rule, name):
+    xb = _all_finite_bf16_rows(32)
+    dq, packed, sc = Q.dynamic_mx_quant(xb, name)
+    x = _bf16_dev(xb, gpu)
+    p, s, d = ops.mxfp4_act_quant(x, rule, dq=torch.empty_like(x))
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy(), sc)
+    assert np.array_equal(p.cpu().numpy(), packed)
+    assert np.array_equal(_bits(d), dq)
+
+
+@pytest.mark.parametrize("rule,name", [(RULE_CEIL_DIV6, "ceil_div6"), (RULE_OCP_FLOOR, "ocp_floor")])
+@pytest.mark.parametrize("scale", [1.0, 1e-30, 1e30])
+def test_mxfp4_quant_random(gpu, rule, name, scale):
+    rng = np.random.default_rng(7)
+    xf = (rng.standard_normal((130, 4096)) * scale).astype(np.float32)
+    xf[5] = 0.0
+    xf[6, :32] = -0.0
+    xb = Q.f32_to_bf16_bits(xf)
+    dq, packed, sc = Q.dynamic_mx_quant(xb, name)
+    x = _bf16_dev(xb, gpu)
+    p, s, d = ops.mxfp4_act_quant(x, rule, dq=torch.empty_like(x))
+    torch.cuda.synchronize()
+    assert np.array_equal(s.cpu().numpy(), sc)
+    assert np.array_equal(p.cpu().numpy(), packed)
+    assert np.array_equal(_bits(d), dq)
+
+
+def test_cpu_tensor_is_rejected(gpu):
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        ops.dequant_mxfp4(torch.zeros(4, 16, dtype=torch.uint8), torch.zeros(4, 1, dtype=torch.uint8))
