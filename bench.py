@@ -1,0 +1,261 @@
+"""Benchmark of the MI355X routed-MoE expert path (one GPU).
+
+Headline workload: bf16-profile MoE decode layer - 256 experts, top-8 routing,
+8 tokens, hidden 4096, expert intermediate 2048 - with every expert's packed
+MXFP4 weights resident in HBM. A step is one pass of the routed layer (align,
+FP8 activation quant, gate/up GEMM + SwiGLU, h quant, down GEMM, combine) over
+one batch of 8 tokens. Eight independent layers' worth of expert weights are
+cycled through so consecutive steps do not re-read the same weights from the
+256 MB last-level cache (a decode step visits every layer once).
+
+Prints ONE JSON line. ``value`` = decode tokens/s through the layer.
+``roofline`` = the dominant kernel (gate/up GEMM) - algorithmic bytes per
+launch over its HIP-event-timed average duration, against 8 TB/s HBM.
+``cpu_baseline`` = the numpy oracle of the same layer on one host core.
+``extra`` = dequant GB/s (config-0 matrices), a4w4 decode (64 tokens) and
+prefill (2048 tokens) in both profiles.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "deepseek-v4-flash-offload_amd"))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MXFP4_PEAK_TFLOPS = 10100.0
+FP8_PEAK_TFLOPS = 5000.0
+BF16_PEAK_TFLOPS = 2500.0
+D, I, E = 4096, 2048, 256
+EXPERT_BYTES = 2 * (I * D // 2 + I * D // 32) + (D * I // 2 + D * I // 32)  # 13,369,344
+GATEUP_BYTES = 2 * (I * D // 2 + I * D // 32)                                  # 8,912,896
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=8, help="distinct expert-weight sets cycled through")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--only", default="", help="profile helper: run only 'decode', 'dequant' or 'prefill'")
+    return ap.parse_args()
+
+
+def gen_layer_weights(dev, n_layers, gen):
+    """Per layer: one contiguous [E, EXPERT_BYTES] pool + its pointer table."""
+    from dsv4_hip import ops
+    pools, tables = [], []
+    offs = {}
+    o = 0
+    for k, n in (("w1p", I * D // 2), ("w1s", I * D // 32), ("w3p", I * D // 2), ("w3s", I * D // 32),
+                 ("w2p", D * I // 2), ("w2s", D * I // 32)):
+        offs[k] = (o, n)
+        o += n
+    for _ in range(n_layers):
+        pool = torch.randint(0, 256, (E, EXPERT_BYTES), dtype=torch.uint8, device=dev, generator=gen)
+        for k in ("w1s", "w3s", "w2s"):  # scale bytes uniform in 117..127
+            a, n = offs[k]
+            pool[:, a:a + n] = torch.randint(117, 128, (E, n), dtype=torch.uint8, device=dev, generator=gen)
+        experts = {e: {k: pool[e, a:a + n] for k, (a, n) in offs.items()} for e in range(E)}
+        pools.append(pool)
+        tables.append(ops.expert_table(experts, E, dev))
+    return pools, tables
+
+
+def routing_batches(n, T, K, seed):
+    from dsv4_hip import synth
+    rng = np.random.default_rng(seed)
+    perm = synth.rank_permutation(E, 3)
+    out = []
+    for i in range(n):
+        ids = synth.zipf_topk(T, K, E, perm, rng)
+        w = synth.routing_weights(T, K, seed + 1000 + i)
+        x = synth.bf16_normal(rng, (T, D))
+        out.append((x, ids, w))
+    return out
+
+
+def time_layer(runner, batches_dev, tables, steps, warmup, profile, rule):
+    n = len(batches_dev)
+    L = len(tables)
+    for i in range(warmup):
+        x, ids, w = batches_dev[i % n]
+        runner.forward(x, ids, w, tables[i % L], profile=profile, rule=rule)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        x, ids, w = batches_dev[i % n]
+        runner.forward(x, ids, w, tables[i % L], profile=profile, rule=rule)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def measure_gemms(batches_dev, batches_host, tables, steps, profile, rule):
+    """Average gate/up and down GEMM durations (HIP events) and algorithmic bytes/flops."""
+    from dsv4_hip import ops, AFMT_E4M3, AFMT_E2M1, PROFILE_BF16
+    n, L = len(batches_dev), len(tables)
+    t_gu, t_dn, b_gu, b_dn, flops = [], [], [], [], []
+    s = torch.cuda.current_stream()
+    for i in range(steps):
+        x, ids, w = batches_dev[i % n]
+        T, K = ids.shape
+        A = len(np.unique(batches_host[i % n][1]))
+        al = ops.moe_align(ids, None, E)
+        fp8 = profile == PROFILE_BF16
+        if fp8:
+            q = ops.fp8_act_quant(x, 128, want_codes=True, want_e8m0x4=True)
+            a, a_s, afmt = q["codes"], q["e8m0x4"], AFMT_E4M3
+        else:
+            a, a_s, _ = ops.mxfp4_act_quant(x, rule)
+            afmt = AFMT_E2M1
+        e0, e1, e2, e3 = (torch.cuda.Event(enable_timing=True) for _ in range(4))
+        e0.record(s)
+        h = ops.gemm_gateup(afmt, a, a_s, K, al, tables[i % L], D, I, w.reshape(-1), 10.0)
+        e1.record(s)
+        if fp8:
+            q = ops.fp8_act_quant(h, 128, want_codes=True, want_e8m0x4=True)
+            ha, has = q["codes"], q["e8m0x4"]
+        else:
+            ha, has, _ = ops.mxfp4_act_quant(h, rule)
+        e2.record(s)
+        ops.gemm_down(afmt, ha, has, al, tables[i % L], I, D)
+        e3.record(s)
+        e3.synchronize()
+        t_gu.append(e0.elapsed_time(e1) * 1e-3)
+        t_dn.append(e2.elapsed_time(e3) * 1e-3)
+        R = T * K
+        a_bytes = T * D * (1 if fp8 else 0.5) + T * D / 32
+        b_gu.append(A * GATEUP_BYTES + a_bytes + 2 * R * I)
+        b_dn.append(A * (EXPERT_BYTES - GATEUP_BYTES) + R * I * ((1 if fp8 else 0.5) + 1 / 32) + 2 * R * D)
+        flops.append(6.0 * R * D * I)
+    k = max(1, steps // 5)  # drop the first fifth (warm-up)
+    return {"t_gateup": float(np.mean(t_gu[k:])), "t_down": float(np.mean(t_dn[k:])),
+            "bytes_gateup": float(np.mean(b_gu[k:])), "bytes_down": float(np.mean(b_dn[k:])),
+            "flops": float(np.mean(flops[k:]))}
+
+
+def measure_dequant(dev, gen, n_mats=64, reps=5):
+    """Config-0 matrices ([2048, 4096] = 2048x2048 packed + 2048x128 scales) dequantised
+    back to back over >= 1.36 GB so the 256 MB last-level cache cannot hold them."""
+    from dsv4_hip import ops
+    N, K = 2048, 4096
+    packed = torch.randint(0, 256, (n_mats, N, K // 2), dtype=torch.uint8, device=dev, generator=gen)
+    scales = torch.randint(117, 128, (n_mats, N, K // 32), dtype=torch.uint8, device=dev, generator=gen)
+    out = torch.empty((n_mats, N, K), dtype=torch.bfloat16, device=dev)
+    for m in range(n_mats):
+        ops.dequant_mxfp4(packed[m], scales[m], out=out[m])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        for m in range(n_mats):
+            ops.dequant_mxfp4(packed[m], scales[m], out=out[m])
+    e1.record()
+    e1.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / (reps * n_mats)
+    per = N * K * 2.53125
+    return {"gbs": per / t / 1e9, "frac_hbm": per / t / 1e9 / HBM_PEAK_GBS, "us_per_matrix": t * 1e6,
+            "bytes_per_matrix": per, "matrices": n_mats}
+
+
+def cpu_baseline(sample_steps=1):
+    """numpy oracle of the same bf16 decode layer (config-1 shapes), one host core."""
+    from threadpoolctl import threadpool_limits
+    from oracle import moe as M
+    from dsv4_hip import synth
+    with threadpool_limits(limits=1):
+        x, ids, w = synth.layer_inputs(8, 8, E, D)
+        xb = x.view(torch.int16).numpy().view(np.uint16)
+        experts = {int(e): synth.expert_weights(int(e), D, I) for e in np.unique(ids)}
+        t0 = time.perf_counter()
+        for _ in range(sample_steps):
+            M.routed_bf16(xb, ids, w, experts, n_experts=E)
+        dt = (time.perf_counter() - t0) / sample_steps
+    return {"value": 8.0 / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{sample_steps} decode step(s) of the numpy oracle (8 tokens, top-8, "
+                      f"{len(experts)} active experts, bf16 profile), 1 thread; {dt:.2f} s/step"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the expert path shards by expert across GPUs, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    from dsv4_hip import ops, PROFILE_A4W4, PROFILE_BF16, RULE_OCP_FLOOR
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+    T, K = 8, 8
+    if args.only in ("", "decode"):
+        pools, tables = gen_layer_weights(dev, args.layers, gen)
+        host = routing_batches(64, T, K, 11)
+        dev_b = [(x.to(dev), torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(dev)) for x, ids, w in host]
+        runner = ops.LayerRunner(dev, E, D, I)
+        torch.cuda.synchronize()
+        s = time_layer(runner, dev_b, tables, args.steps, args.warmup, PROFILE_BF16, RULE_OCP_FLOOR)
+        gm = measure_gemms(dev_b, host, tables, min(args.steps, 100), PROFILE_BF16, RULE_OCP_FLOOR)
+        ach = gm["bytes_gateup"] / gm["t_gateup"] / 1e9
+        line = {
+            "metric": "MoE decode tok/s (bf16 profile, 256 experts top-8, hidden 4096, inter 2048)",
+            "value": T / s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": s * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "fp8e4m3 x mxfp4 (fp32 accumulate)", "data": "synthetic",
+            "config": {"workload": "bf16-profile MoE decode layer: 8 tokens, 256 experts, top-8 Zipf(1.1), "
+                                   "hidden 4096, inter 2048, MXFP4 experts resident in HBM",
+                       "tokens": T, "topk": K, "experts": E, "hidden": D, "inter": I,
+                       "weight_sets_cycled": args.layers},
+            "roofline": {"bound": "hbm", "kernel": "moe_gemm_kernel<E4M3, gate/up>", "achieved": ach,
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": ach / HBM_PEAK_GBS, "traffic": None,
+                         "algorithmic_bytes_per_launch": gm["bytes_gateup"],
+                         "avg_launch_us": gm["t_gateup"] * 1e6},
+            "gemm": {"gateup_us": gm["t_gateup"] * 1e6, "down_us": gm["t_down"] * 1e6,
+                     "down_gbs": gm["bytes_down"] / gm["t_down"] / 1e9,
+                     "layer_tflops": gm["flops"] / s / 1e12},
+        }
+        del pools, tables
+        torch.cuda.empty_cache()
+    else:
+        line = {"metric": "profile helper", "value": None}
+    extra = {}
+    if not args.no_extra and args.only in ("", "dequant"):
+        extra["dequant_config0"] = measure_dequant(dev, gen)
+        torch.cuda.empty_cache()
+    if not args.no_extra and args.only in ("", "prefill"):
+        pools, tables = gen_layer_weights(dev, 2, gen)
+        runner = ops.LayerRunner(dev, E, D, I)
+        for name, Tn, prof in (("a4w4_decode_64", 64, PROFILE_A4W4), ("bf16_prefill_2048", 2048, PROFILE_BF16),
+                               ("a4w4_prefill_2048", 2048, PROFILE_A4W4)):
+            host = routing_batches(4, Tn, K, 21 + Tn)
+            dev_b = [(x.to(dev), torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(dev))
+                     for x, ids, w in host]
+            st = 20 if Tn <= 64 else 5
+            s2 = time_layer(runner, dev_b, tables, st, 3, prof, RULE_OCP_FLOOR)
+            A = float(np.mean([len(np.unique(b[1])) for b in host]))
+            flops = 6.0 * Tn * K * D * I
+            byts = A * EXPERT_BYTES + 4 * Tn * D
+            peak = MXFP4_PEAK_TFLOPS if prof == PROFILE_A4W4 else FP8_PEAK_TFLOPS
+            extra[name] = {"ms_per_layer": s2 * 1e3, "tokens_per_s": Tn / s2, "tflops": flops / s2 / 1e12,
+                           "frac_mfma_peak": flops / s2 / 1e12 / peak, "hbm_gbs": byts / s2 / 1e9,
+                           "frac_hbm": byts / s2 / 1e9 / HBM_PEAK_GBS, "active_experts": A}
+        del pools, tables
+        torch.cuda.empty_cache()
+    if extra:
+        line["extra"] = extra
+    if not args.no_cpu_baseline and args.only == "":
+        line["cpu_baseline"] = cpu_baseline()
+        line["cpu_baseline"]["host_threads_available"] = os.cpu_count()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

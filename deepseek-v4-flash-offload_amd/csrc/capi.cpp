@@ -175,8 +175,8 @@ static int check_gemm_common(int afmt, const void* a, const void* a_scale, const
   REQUIRE(afmt == DSV4_AFMT_E4M3 || afmt == DSV4_AFMT_E2M1, DSV4_ERR_UNSUPPORTED, "gemm: unknown A format %d",
           afmt);
   REQUIRE(R >= 0 && max_blocks >= 0, DSV4_ERR_SHAPE, "gemm: negative size");
-  REQUIRE(Kdim > 0 && Kdim % 512 == 0, DSV4_ERR_UNSUPPORTED, "gemm: reduction dim %d not a multiple of 512",
-          Kdim);
+  REQUIRE(moe_gemm_supported_kdim(Kdim), DSV4_ERR_UNSUPPORTED,
+          "gemm: reduction dim %d unsupported (512, 1024, 2048, 4096 or 8192)", Kdim);
   REQUIRE(a && a_scale && sorted_ids && block_expert && npp && experts && out, DSV4_ERR_NULL,
           "gemm: null pointer");
   REQUIRE(aligned(a, 16) && aligned(a_scale, 4) && aligned(experts, 8), DSV4_ERR_SHAPE,
@@ -190,7 +190,7 @@ int dsv4_moe_gemm_gateup(int afmt, const void* a, const void* a_scale, int a_row
                          float swiglu_limit, void* h_out, void* stream) {
   REQUIRE(block_m == DSV4_GEMM_BLOCK_M, DSV4_ERR_UNSUPPORTED, "gemm: block_m %d unsupported (%d)", block_m,
           DSV4_GEMM_BLOCK_M);
-  REQUIRE(I > 0 && I % 64 == 0, DSV4_ERR_UNSUPPORTED, "gemm gate/up: I=%d not a multiple of 64", I);
+  REQUIRE(I > 0 && I % 128 == 0, DSV4_ERR_UNSUPPORTED, "gemm gate/up: I=%d not a multiple of 128", I);
   REQUIRE(a_row_div > 0, DSV4_ERR_SHAPE, "gemm gate/up: a_row_div=%d", a_row_div);
   if (R == 0 || max_blocks == 0) return DSV4_OK;
   int rc = check_gemm_common(afmt, a, a_scale, sorted_ids, block_expert, num_post_padded, R, max_blocks,
@@ -209,7 +209,7 @@ int dsv4_moe_gemm_down(int afmt, const void* a, const void* a_scale, const int32
                        int max_blocks, const void* expert_table, int I, int D, void* out, void* stream) {
   REQUIRE(block_m == DSV4_GEMM_BLOCK_M, DSV4_ERR_UNSUPPORTED, "gemm: block_m %d unsupported (%d)", block_m,
           DSV4_GEMM_BLOCK_M);
-  REQUIRE(D > 0 && D % 128 == 0, DSV4_ERR_UNSUPPORTED, "gemm down: D=%d not a multiple of 128", D);
+  REQUIRE(D > 0 && D % 256 == 0, DSV4_ERR_UNSUPPORTED, "gemm down: D=%d not a multiple of 256", D);
   if (R == 0 || max_blocks == 0) return DSV4_OK;
   int rc = check_gemm_common(afmt, a, a_scale, sorted_ids, block_expert, num_post_padded, R, max_blocks,
                              expert_table, I, out);

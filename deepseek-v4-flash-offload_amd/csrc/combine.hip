@@ -45,13 +45,14 @@ DSV4_DEV u32x4 pack8(const float* acc) {
   return r;
 }
 
-// One workgroup per token. The token's K entries are ordered by (key, k) with
-// an insertion sort that every thread performs identically.
+// Workgroups of 64 lanes tile (token, 512-column chunk); each lane owns 8
+// columns. The token's K entries are ordered by (key, k) with an insertion sort
+// that every lane performs identically.
 template <typename IdT>
-__global__ __launch_bounds__(256) void combine_flat_kernel(const u32x4* __restrict__ src,
-                                                           const IdT* __restrict__ ids, int K, int D,
-                                                           u32x4* __restrict__ y) {
-  const int t = blockIdx.x;
+__global__ __launch_bounds__(64) void combine_flat_kernel(const u32x4* __restrict__ src,
+                                                          const IdT* __restrict__ ids, int K, int D,
+                                                          u32x4* __restrict__ y) {
+  const int t = blockIdx.y;
   int ord[kMaxK];
   long long key[kMaxK];
   for (int k = 0; k < K; ++k) {
@@ -61,11 +62,11 @@ __global__ __launch_bounds__(256) void combine_flat_kernel(const u32x4* __restri
     key[j] = kk; ord[j] = k;
   }
   const int vecs = D / 8;
-  for (int c = threadIdx.x; c < vecs; c += 256) {
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < K; ++j) accumulate8(acc, src[((int64_t)t * K + ord[j]) * vecs + c]);
-    y[(int64_t)t * vecs + c] = pack8(acc);
-  }
+  const int c = blockIdx.x * 64 + threadIdx.x;
+  if (c >= vecs) return;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < K; ++j) accumulate8(acc, src[((int64_t)t * K + ord[j]) * vecs + c]);
+  y[(int64_t)t * vecs + c] = pack8(acc);
 }
 
 __global__ __launch_bounds__(256) void bucket_rows_kernel(const int32_t* __restrict__ row, int R, int T, int Kmax,
@@ -120,12 +121,13 @@ hipError_t launch_moe_gather_rows(const uint8_t* src, int64_t n_src, const int32
 
 hipError_t launch_moe_combine_flat(const uint16_t* src, const void* topk_ids, int ids_int64, int T, int K,
                                    int D, uint16_t* y, hipStream_t st) {
-  if (T == 0) return hipSuccess;
+  if (T == 0 || D == 0) return hipSuccess;
+  const dim3 grid((D / 8 + 63) / 64, T);
   if (ids_int64)
-    hipLaunchKernelGGL(combine_flat_kernel<long long>, dim3(T), dim3(256), 0, st, (const u32x4*)src,
+    hipLaunchKernelGGL(combine_flat_kernel<long long>, grid, dim3(64), 0, st, (const u32x4*)src,
                        (const long long*)topk_ids, K, D, (u32x4*)y);
   else
-    hipLaunchKernelGGL(combine_flat_kernel<int32_t>, dim3(T), dim3(256), 0, st, (const u32x4*)src,
+    hipLaunchKernelGGL(combine_flat_kernel<int32_t>, grid, dim3(64), 0, st, (const u32x4*)src,
                        (const int32_t*)topk_ids, K, D, (u32x4*)y);
   return hipGetLastError();
 }

@@ -14,18 +14,21 @@
 //    tolerance rather than bit equality on GEMM outputs).
 //  * a4w4 profile: FP4 x FP4 with per-32 E8M0 scales on both operands.
 //
-// Work decomposition: one workgroup = 4 waves = one M block (16 padded rows of
-// one expert, from moe_align) x one N tile. The A rows are gathered on load
-// through sorted_ids (no permuted copy of x is materialised). Every wave owns
-// two 16x16 output tiles and streams their weight rows straight from HBM into
-// registers (each weight byte is used by exactly one wave, so LDS staging would
-// only add traffic); the next 512-wide K step is prefetched while the current
-// one is multiplied.
+// Work decomposition: one single-wave workgroup = one M block (16 padded rows of
+// one expert, from moe_align) x NT = 4 output tiles of 16 columns (gate/up: 2
+// gate + 2 up tiles of the same 32 intermediate columns). Small workgroups keep
+// the per-CU load even (a decode step has ~40 active experts x 64 column
+// chunks = ~2560 workgroups for 256 CUs). The A rows are gathered on load
+// through sorted_ids (no permuted copy of x is materialised). The wave streams
+// its weight rows straight from HBM into registers: every weight byte is used
+// by exactly one wave, so staging it through LDS would only add traffic. The K
+// loop runs in 256-wide stages with a two-stage register ring and no branches,
+// so the loads of stage j+1 are in flight while stage j is multiplied.
 //
-// K mapping. One 512-wide K step is 4 MFMAs (ji = 0..3) of 128 logical k each.
-// Logical 32-block b of MFMA ji is global 32-block 16*jo + 4*b + ji, so the
-// lane holding block b of a B row (lane group g = b) reads 64 contiguous bytes
-// (4 x 16 B) per K step and its 4 scale bytes are one aligned dword.
+// K mapping. One 256-wide stage is 2 MFMAs (ji = 0, 1) of 128 logical k. Logical
+// 32-block b of MFMA ji is global 32-block 8*j + 2*b + ji, so the lane holding
+// block b of a weight row (lane group g = b) reads 32 contiguous bytes per stage
+// and the four lane groups of a row read its 128 contiguous bytes.
 // Operand layouts (measured on gfx950):
 //   E2M1 A/B: lane (r = l%16, g = l/16) holds logical k [32g, 32g+32) of row r
 //             in 16 bytes, low nibble first.
@@ -39,138 +42,173 @@
 namespace {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#ifndef DSV4_GEMM_PREFETCH
+#define DSV4_GEMM_PREFETCH 1
+#endif
+#ifndef DSV4_GEMM_NT_LOADS
+#define DSV4_GEMM_NT_LOADS 0
+#endif
 
 constexpr int kBM = 16;
+constexpr int kNT = 4;        // 16-column output tiles per wave
+#ifndef DSV4_GEMM_WAVES
+#define DSV4_GEMM_WAVES 1
+#endif
+constexpr int kWaves = DSV4_GEMM_WAVES;  // waves per workgroup (they share nothing but the M block)
+constexpr int kStageK = 256;  // reduction elements per pipeline stage
 
 template <int AFMT>
-struct AFrag {
-  u32x4 v[AFMT == 0 ? 8 : 4];
+struct AStage;
+template <>
+struct AStage<0> {  // E4M3: 32 bytes per lane per MFMA
+  v8i d[2];
   uint32_t s;
 };
-struct BFrag {
-  u32x4 v[2][4];
-  uint32_t s[2];
+template <>
+struct AStage<1> {  // E2M1: 16 bytes per lane per MFMA
+  v4i d[2];
+  uint32_t s;
+};
+struct BStage {
+  v4i d[kNT][2];
+  uint32_t s[kNT];
 };
 
+// Every operand lives in global memory; the casts keep the loads global_load_*
+// (pointers read from the expert table would otherwise become flat accesses).
+typedef __attribute__((address_space(1))) const v4i gv4i;
+typedef __attribute__((address_space(1))) const uint16_t gu16;
+DSV4_DEV v4i ld16(const uint8_t* p) { return *(gv4i*)p; }
+#if DSV4_GEMM_NT_LOADS
+DSV4_DEV v4i ld16_stream(const uint8_t* p) { return __builtin_nontemporal_load((gv4i*)p); }
+#else
+// plain loads: measured faster than non-temporal ones for this pattern on MI355X
+DSV4_DEV v4i ld16_stream(const uint8_t* p) { return *(gv4i*)p; }
+#endif
+DSV4_DEV uint32_t ld_u16(const uint8_t* p) { return *(gu16*)p; }
+
 template <int AFMT>
-DSV4_DEV void load_a(AFrag<AFMT>& a, const uint8_t* abase, const uint8_t* asbase, bool ok, int jo, int g) {
-  if (!ok) {
-#pragma unroll
-    for (int i = 0; i < (AFMT == 0 ? 8 : 4); ++i) a.v[i] = u32x4{0u, 0u, 0u, 0u};
-    a.s = 0x7f7f7f7fu;
-    return;
-  }
-  if (AFMT == 1) {
-    const u32x4* p = (const u32x4*)(abase + (int64_t)jo * 256 + g * 64);
-#pragma unroll
-    for (int ji = 0; ji < 4; ++ji) a.v[ji] = p[ji];
+DSV4_DEV void load_a(AStage<AFMT>& a, const uint8_t* abase, const uint8_t* asbase, int j, int g) {
+  if constexpr (AFMT == 1) {
+    const uint8_t* p = abase + (int64_t)j * 128 + g * 32;
+    a.d[0] = ld16(p);
+    a.d[1] = ld16(p + 16);
   } else {
-    const uint8_t* p = abase + (int64_t)jo * 512 + 16 * (g & 1);
+    const uint8_t* p = abase + (int64_t)j * 256 + 16 * (g & 1) + 64 * (g >> 1);
 #pragma unroll
-    for (int ji = 0; ji < 4; ++ji) {
-      a.v[2 * ji] = *(const u32x4*)(p + 128 * (g >> 1) + 32 * ji);
-      a.v[2 * ji + 1] = *(const u32x4*)(p + 128 * (2 + (g >> 1)) + 32 * ji);
+    for (int ji = 0; ji < 2; ++ji) {
+      const v4i lo = ld16(p + 32 * ji);        // logical block g>>1
+      const v4i hi = ld16(p + 32 * ji + 128);  // logical block 2 + (g>>1)
+      a.d[ji] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     }
   }
-  a.s = *(const uint32_t*)(asbase + jo * 16 + 4 * g);
+  a.s = ld_u16(asbase + j * 8 + 2 * g);
 }
 
-DSV4_DEV void load_b(BFrag& b, const uint8_t* b0, const uint8_t* bs0, const uint8_t* b1, const uint8_t* bs1,
-                     int jo, int g) {
-  const u32x4* p0 = (const u32x4*)(b0 + (int64_t)jo * 256 + g * 64);
-  const u32x4* p1 = (const u32x4*)(b1 + (int64_t)jo * 256 + g * 64);
+DSV4_DEV void load_b(BStage& b, const uint8_t* const* bt, const uint8_t* const* bst, int j, int g) {
 #pragma unroll
-  for (int ji = 0; ji < 4; ++ji) {
-    b.v[0][ji] = __builtin_nontemporal_load(p0 + ji);
-    b.v[1][ji] = __builtin_nontemporal_load(p1 + ji);
-  }
-  b.s[0] = *(const uint32_t*)(bs0 + jo * 16 + 4 * g);
-  b.s[1] = *(const uint32_t*)(bs1 + jo * 16 + 4 * g);
-}
-
-template <int AFMT, int JI>
-DSV4_DEV void mfma_step(v4f* acc, const AFrag<AFMT>& a, const BFrag& b) {
-  v8i av;
-  if (AFMT == 1) {
-    av = v8i{(int)a.v[JI].x, (int)a.v[JI].y, (int)a.v[JI].z, (int)a.v[JI].w, 0, 0, 0, 0};
-  } else {
-    const u32x4 lo = a.v[2 * JI], hi = a.v[2 * JI + 1];
-    av = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-  }
-  const int sa = (int)((a.s >> (8 * JI)) & 0xffu);
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const v8i bv = v8i{(int)b.v[t][JI].x, (int)b.v[t][JI].y, (int)b.v[t][JI].z, (int)b.v[t][JI].w, 0, 0, 0, 0};
-    const int sb = (int)((b.s[t] >> (8 * JI)) & 0xffu);
-    acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc[t], AFMT == 0 ? 0 : 4, 4, 0, sa, 0, sb);
+  for (int t = 0; t < kNT; ++t) {
+    const uint8_t* p = bt[t] + (int64_t)j * 128 + g * 32;
+    b.d[t][0] = ld16_stream(p);
+    b.d[t][1] = ld16_stream(p + 16);
+    b.s[t] = ld_u16(bst[t] + j * 8 + 2 * g);
   }
 }
 
 template <int AFMT>
-DSV4_DEV void mfma_kstep(v4f* acc, const AFrag<AFMT>& a, const BFrag& b) {
-  mfma_step<AFMT, 0>(acc, a, b);
-  mfma_step<AFMT, 1>(acc, a, b);
-  mfma_step<AFMT, 2>(acc, a, b);
-  mfma_step<AFMT, 3>(acc, a, b);
+DSV4_DEV void compute(v4f* acc, const AStage<AFMT>& a, const BStage& b) {
+#pragma unroll
+  for (int ji = 0; ji < 2; ++ji) {
+    v8i av;
+    if constexpr (AFMT == 1) {
+      av = v8i{a.d[ji].x, a.d[ji].y, a.d[ji].z, a.d[ji].w, 0, 0, 0, 0};
+    } else {
+      av = a.d[ji];
+    }
+    const int sa = (int)((a.s >> (8 * ji)) & 0xffu);
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) {
+      const v8i bv = v8i{b.d[t][ji].x, b.d[t][ji].y, b.d[t][ji].z, b.d[t][ji].w, 0, 0, 0, 0};
+      const int sb = (int)((b.s[t] >> (8 * ji)) & 0xffu);
+      acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc[t], AFMT == 0 ? 0 : 4, 4, 0, sa, 0, sb);
+    }
+  }
 }
 
-template <int AFMT, bool GATEUP>
-__global__ __launch_bounds__(256) void moe_gemm_kernel(Dsv4GemmArgs p) {
+template <int AFMT, bool GATEUP, int NST>
+__global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int mb = blockIdx.y;
   if (mb * kBM >= p.num_post_padded[0]) return;
   const int e = p.block_expert[mb];
   const Dsv4ExpertPtrs ex = p.experts[e];
-  const int r16 = lane & 15, g = lane >> 4;
-  // An expert whose weights are not in the table contributes zeros (never read null).
+  // an expert whose weights are not in the table contributes zeros (never read null)
   const bool have_w = GATEUP ? (ex.w1p && ex.w1s && ex.w3p && ex.w3s) : (ex.w2p && ex.w2s);
+  const int r16 = lane & 15, g = lane >> 4;
 
-  // A operand row of this lane (gather on load).
+  // A operand row of this lane, gathered on load. Padding rows read row 0:
+  // their products land only in output rows that are never stored.
   const int f_in = p.sorted_ids[mb * kBM + r16];
-  const bool a_ok = f_in < p.R;
-  const int64_t arow = a_ok ? (int64_t)(f_in / p.a_row_div) : 0;
+  const int64_t arow = f_in < p.R ? (int64_t)(f_in / p.a_row_div) : 0;
   const uint8_t* abase = p.a + arow * p.a_row_bytes;
   const uint8_t* asbase = p.a_scale + arow * (int64_t)(p.Kdim / 32);
 
-  // B rows of this lane's two 16-row weight tiles.
+  // weight rows of this lane's tiles
   const int64_t brow_bytes = p.Kdim / 2, bsrow = p.Kdim / 32;
   int col0;
-  const uint8_t *b0, *bs0, *b1, *bs1;
+  const uint8_t* bt[kNT];
+  const uint8_t* bst[kNT];
   if (GATEUP) {
-    col0 = blockIdx.x * 64 + wave * 16;  // output column of gate tile and up tile
-    b0 = ex.w1p + (int64_t)(col0 + r16) * brow_bytes;
-    bs0 = ex.w1s + (int64_t)(col0 + r16) * bsrow;
-    b1 = ex.w3p + (int64_t)(col0 + r16) * brow_bytes;
-    bs1 = ex.w3s + (int64_t)(col0 + r16) * bsrow;
+    col0 = blockIdx.x * (kWaves * 32) + wave * 32;  // 32 intermediate columns: 2 gate + 2 up tiles
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int64_t row = col0 + 16 * t + r16;
+      bt[t] = ex.w1p + row * brow_bytes;
+      bst[t] = ex.w1s + row * bsrow;
+      bt[t + 2] = ex.w3p + row * brow_bytes;
+      bst[t + 2] = ex.w3s + row * bsrow;
+    }
   } else {
-    col0 = blockIdx.x * 128 + wave * 32;
-    b0 = ex.w2p + (int64_t)(col0 + r16) * brow_bytes;
-    bs0 = ex.w2s + (int64_t)(col0 + r16) * bsrow;
-    b1 = ex.w2p + (int64_t)(col0 + 16 + r16) * brow_bytes;
-    bs1 = ex.w2s + (int64_t)(col0 + 16 + r16) * bsrow;
+    col0 = blockIdx.x * (kWaves * 64) + wave * 64;
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) {
+      const int64_t row = col0 + 16 * t + r16;
+      bt[t] = ex.w2p + row * brow_bytes;
+      bst[t] = ex.w2s + row * bsrow;
+    }
   }
 
-  v4f acc[2] = {v4f{0.f, 0.f, 0.f, 0.f}, v4f{0.f, 0.f, 0.f, 0.f}};
-  const int njo = have_w ? p.Kdim / 512 : 0;
-  AFrag<AFMT> a0, a1;
-  BFrag w0, w1;
-  if (njo > 0) {
-    load_a<AFMT>(a0, abase, asbase, a_ok, 0, g);
-    load_b(w0, b0, bs0, b1, bs1, 0, g);
-  }
-  for (int jo = 0; jo < njo; jo += 2) {
-    if (jo + 1 < njo) {
-      load_a<AFMT>(a1, abase, asbase, a_ok, jo + 1, g);
-      load_b(w1, b0, bs0, b1, bs1, jo + 1, g);
+  v4f acc[kNT];
+#pragma unroll
+  for (int t = 0; t < kNT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  if (have_w) {
+    // NST = Kdim / 256 stages, fully unrolled into straight-line code. With
+    // DSV4_GEMM_PREFETCH = P > 0 the loads of stage j+P are issued before the
+    // MFMAs of stage j and a scheduling barrier keeps them there (a P+1 deep
+    // register ring); with P = 0 the compiler schedules freely.
+    constexpr int P = DSV4_GEMM_PREFETCH;
+    constexpr int RING = P + 1;
+    AStage<AFMT> a[RING];
+    BStage b[RING];
+#pragma unroll
+    for (int j = 0; j < P && j < NST; ++j) {
+      load_a<AFMT>(a[j % RING], abase, asbase, j, g);
+      load_b(b[j % RING], bt, bst, j, g);
     }
-    mfma_kstep<AFMT>(acc, a0, w0);
-    if (jo + 2 < njo) {
-      load_a<AFMT>(a0, abase, asbase, a_ok, jo + 2, g);
-      load_b(w0, b0, bs0, b1, bs1, jo + 2, g);
+#pragma unroll
+    for (int j = 0; j < NST; ++j) {
+      if (j + P < NST) {
+        load_a<AFMT>(a[(j + P) % RING], abase, asbase, j + P, g);
+        load_b(b[(j + P) % RING], bt, bst, j + P, g);
+      }
+      if constexpr (P > 0) __builtin_amdgcn_sched_barrier(0);
+      compute<AFMT>(acc, a[j % RING], b[j % RING]);
+      if constexpr (P > 0) __builtin_amdgcn_sched_barrier(0);
     }
-    if (jo + 1 < njo) mfma_kstep<AFMT>(acc, a1, w1);
   }
 
   // Epilogue: lane holds rows 4*g + i (i = 0..3) of column r16 of each tile.
@@ -178,39 +216,60 @@ __global__ __launch_bounds__(256) void moe_gemm_kernel(Dsv4GemmArgs p) {
   for (int i = 0; i < 4; ++i) {
     const int f = p.sorted_ids[mb * kBM + 4 * g + i];
     if (f >= p.R) continue;
+    uint16_t* orow = p.out + (int64_t)f * p.N + col0 + r16;
     if (GATEUP) {
-      // deepseek_v4.py:177-187: bf16 GEMM outputs -> fp32, clamp, silu(gate)*up*w
-      float gt = dsv4::bf16_to_f32(dsv4::f32_to_bf16(acc[0][i]));
-      float up = dsv4::bf16_to_f32(dsv4::f32_to_bf16(acc[1][i]));
-      if (p.swiglu_limit > 0.0f) {
-        up = fminf(fmaxf(up, -p.swiglu_limit), p.swiglu_limit);
-        gt = fminf(gt, p.swiglu_limit);
+      // deepseek_v4.py:177-187: bf16 GEMM outputs -> fp32, clamp, silu(gate) * up * w
+      const float w = p.topk_w[f];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float gt = dsv4::bf16_to_f32(dsv4::f32_to_bf16(acc[t][i]));
+        float up = dsv4::bf16_to_f32(dsv4::f32_to_bf16(acc[t + 2][i]));
+        if (p.swiglu_limit > 0.0f) {
+          up = fminf(fmaxf(up, -p.swiglu_limit), p.swiglu_limit);
+          gt = fminf(gt, p.swiglu_limit);
+        }
+        const float h = gt / (1.0f + expf(-gt)) * up * w;
+        orow[16 * t] = (uint16_t)dsv4::f32_to_bf16(h);
       }
-      const float h = gt / (1.0f + __expf(-gt)) * up * p.topk_w[f];
-      p.out[(int64_t)f * p.N + col0 + r16] = (uint16_t)dsv4::f32_to_bf16(h);
     } else {
-      p.out[(int64_t)f * p.N + col0 + r16] = (uint16_t)dsv4::f32_to_bf16(acc[0][i]);
-      p.out[(int64_t)f * p.N + col0 + 16 + r16] = (uint16_t)dsv4::f32_to_bf16(acc[1][i]);
+#pragma unroll
+      for (int t = 0; t < kNT; ++t) orow[16 * t] = (uint16_t)dsv4::f32_to_bf16(acc[t][i]);
     }
   }
 }
 
 }  // namespace
 
-hipError_t launch_moe_gemm_gateup(const Dsv4GemmArgs& a, hipStream_t st) {
-  dim3 grid(a.N / 64, a.max_blocks);
+template <bool GATEUP, int NST>
+static void launch_nst(const Dsv4GemmArgs& a, dim3 grid, hipStream_t st) {
   if (a.afmt == 0)
-    hipLaunchKernelGGL((moe_gemm_kernel<0, true>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((moe_gemm_kernel<0, GATEUP, NST>), grid, dim3(64 * kWaves), 0, st, a);
   else
-    hipLaunchKernelGGL((moe_gemm_kernel<1, true>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((moe_gemm_kernel<1, GATEUP, NST>), grid, dim3(64 * kWaves), 0, st, a);
+}
+
+template <bool GATEUP>
+static hipError_t launch(const Dsv4GemmArgs& a, dim3 grid, hipStream_t st) {
+  switch (a.Kdim / kStageK) {
+    case 2: launch_nst<GATEUP, 2>(a, grid, st); break;
+    case 4: launch_nst<GATEUP, 4>(a, grid, st); break;
+    case 8: launch_nst<GATEUP, 8>(a, grid, st); break;
+    case 16: launch_nst<GATEUP, 16>(a, grid, st); break;
+    case 32: launch_nst<GATEUP, 32>(a, grid, st); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
+bool moe_gemm_supported_kdim(int kdim) {
+  const int n = kdim / kStageK;
+  return kdim % kStageK == 0 && (n == 2 || n == 4 || n == 8 || n == 16 || n == 32);
+}
+
+hipError_t launch_moe_gemm_gateup(const Dsv4GemmArgs& a, hipStream_t st) {
+  return launch<true>(a, dim3(a.N / (kWaves * 32), a.max_blocks), st);
+}
+
 hipError_t launch_moe_gemm_down(const Dsv4GemmArgs& a, hipStream_t st) {
-  dim3 grid(a.N / 128, a.max_blocks);
-  if (a.afmt == 0)
-    hipLaunchKernelGGL((moe_gemm_kernel<0, false>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((moe_gemm_kernel<1, false>), grid, dim3(256), 0, st, a);
-  return hipGetLastError();
+  return launch<false>(a, dim3(a.N / (kWaves * 64), a.max_blocks), st);
 }

@@ -47,6 +47,25 @@ SIGNATURES = {
     "dsv4_moe_layer_workspace_bytes": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i64)]),
     "dsv4_moe_layer_forward": (_i32, [_i32, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32, _c_p,
                                       _f32, _c_p, _i64, _c_p, _c_p]),
+    # slot cache
+    "dsv4_lru_create": (_i32, [_i32, ctypes.POINTER(_c_p)]),
+    "dsv4_lru_destroy": (_i32, [_c_p]),
+    "dsv4_lru_access": (_i32, [_c_p, _i64, ctypes.POINTER(_i32), ctypes.POINTER(_i32), ctypes.POINTER(_i64)]),
+    "dsv4_lru_keys": (_i32, [_c_p, _c_p, _i32, ctypes.POINTER(_i32)]),
+    "dsv4_slots_create": (_i32, [_i32, _i64, _i32, _c_p, _i32, ctypes.POINTER(_c_p)]),
+    "dsv4_slots_destroy": (_i32, [_c_p]),
+    "dsv4_slots_host_record": (_i32, [_c_p, _i32, _i32, _i32, ctypes.POINTER(_c_p), ctypes.POINTER(_i32)]),
+    "dsv4_slots_num_registered": (_i32, [_c_p, ctypes.POINTER(_i64)]),
+    "dsv4_slots_acquire": (_i32, [_c_p, _i32, _c_p, _i32, _c_p, _c_p, ctypes.POINTER(_i32)]),
+    "dsv4_slots_prefetch": (_i32, [_c_p, _i32, _c_p, _i32, ctypes.POINTER(_i32)]),
+    "dsv4_slots_release": (_i32, [_c_p, _c_p]),
+    "dsv4_slots_copy_record": (_i32, [_c_p, _i32, _i32, _c_p, _c_p]),
+    "dsv4_slots_lookup": (_i32, [_c_p, _i32, _i32, ctypes.POINTER(_i32)]),
+    "dsv4_slots_keys": (_i32, [_c_p, _c_p, _i32, ctypes.POINTER(_i32)]),
+    "dsv4_slots_sync": (_i32, [_c_p]),
+    "dsv4_slots_invalidate": (_i32, [_c_p]),
+    "dsv4_slots_stats": (_i32, [_c_p, _c_p]),
+    "dsv4_slots_reset_stats": (_i32, [_c_p]),
 }
 
 _LIB = None

@@ -1,0 +1,268 @@
+"""DeepSeek-V4 MoE takeover with offloaded experts, computed by the HIP expert path.
+
+Surface of ``dsv4_plugin/models/deepseek_v4.py`` in the reference:
+``OffloadDeepseekV4MoE(config, parallel_config, quant_config=None, prefix="",
+is_draft_layer=False)`` with ``_route`` / ``_routed`` / ``_routed_mxfp4`` /
+``forward``, the module toggle ``_MXFP4_GMM`` (read at call time, env
+``DSV4_MXFP4_GMM``), ``_offload_load_weights``, ``_ORIG_LOAD_WEIGHTS`` and
+``install_patches``.
+
+Routing (``_route``) keeps the reference's torch math on the device. The
+routed experts run as ONE call into ``libdsv4hip.so``
+(``dsv4_moe_layer_forward``): moe_align, activation quantisation, the grouped
+gate/up GEMM with the SwiGLU epilogue, the h quantisation, the grouped down
+GEMM and the deterministic combine. Expert weights are read in place from the
+engine's packed slots through a device pointer table (no restacking, no
+per-expert host sync).
+
+vLLM is optional: when a DeepSeek-V4 model module is importable the class
+derives from its ``DeepseekV4MoE`` and ``install_patches`` swaps it in;
+otherwise the class is a plain ``nn.Module`` (shared experts omitted) and
+``install_patches`` is a no-op.
+"""
+
+import importlib
+import os
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from dsv4_plugin.core.engine import get_engine, is_expert_weight
+from dsv4_hip import ops as _ops
+from dsv4_hip import _lib
+
+_V4_MODULES = ("vllm_ascend.models.deepseek_v4", "vllm.model_executor.models.deepseek_v4")
+
+
+def _find_v4():
+    for name in _V4_MODULES:
+        try:
+            return importlib.import_module(name)
+        except Exception:  # noqa: BLE001 - any import failure means "not available"
+            continue
+    return None
+
+
+v4 = _find_v4()
+
+_PATCHED = False
+_MXFP4_GMM = os.environ.get("DSV4_MXFP4_GMM", "0") == "1"
+# activation scale rule of the a4w4 profile: "ocp_floor" or "ceil_div6"
+_MX_RULE = os.environ.get("DSV4_MX_RULE", "ocp_floor")
+_RULES = {"ocp_floor": _lib.RULE_OCP_FLOOR, "ceil_div6": _lib.RULE_CEIL_DIV6}
+
+_BASE = v4.DeepseekV4MoE if (v4 is not None and hasattr(v4, "DeepseekV4MoE")) else nn.Module
+_RUNNERS = {}
+
+
+def _runner(device, E, D, I):
+    key = (str(device), E, D, I)
+    r = _RUNNERS.get(key)
+    if r is None:
+        r = _RUNNERS[key] = _ops.LayerRunner(device, E, D, I)
+    return r
+
+
+class _ExpertsFacade:
+    """Stand-in for the FusedMoE experts object that vLLM code may touch."""
+
+    is_internal_router = False
+
+    def __init__(self, moe):
+        self._moe = moe
+
+    def update_expert_map(self):
+        pass
+
+
+class _Gate(nn.Module):
+    """Router parameters when vLLM is absent: fp32 weight [E, D], bias or tid2eid."""
+
+    def __init__(self, hidden, n_experts):
+        super().__init__()
+        self.weight = nn.Parameter(torch.zeros(n_experts, hidden, dtype=torch.float32), requires_grad=False)
+        self.e_score_correction_bias = None
+        self.tid2eid = None
+
+
+class OffloadDeepseekV4MoE(_BASE):
+    """Routed MoE layer whose experts live in host memory and device slots."""
+
+    def __init__(self, config, parallel_config, quant_config=None, prefix="", is_draft_layer=False):
+        nn.Module.__init__(self)  # the base __init__ would place every expert on the device
+        self.tp_size = v4.get_tensor_model_parallel_world_size() if v4 is not None else 1
+        self.tp_rank = v4.get_tensor_model_parallel_rank() if v4 is not None else 0
+        self.layer_idx = int(prefix.split(sep=".")[-2])
+        self.routed_scaling_factor = getattr(config, "routed_scaling_factor", 1.5)
+        self.swiglu_limit = getattr(config, "swiglu_limit", None)
+        self.n_routed_experts = config.n_routed_experts
+        self.n_shared_experts = config.n_shared_experts
+        self.topk = config.num_experts_per_tok
+        self.renormalize = config.norm_topk_prob
+        self.num_expert_group = getattr(config, "n_group", 1)
+        self.topk_group = getattr(config, "topk_group", 1)
+        self.scoring_func = getattr(config, "scoring_func", "softmax")
+        self.is_sequence_parallel = getattr(parallel_config, "use_sequence_parallel_moe", False)
+        if v4 is not None:
+            self.gate = v4.ReplicatedLinear(config.hidden_size, config.n_routed_experts, bias=False,
+                                            quant_config=None, prefix=f"{prefix}.gate")
+            self.gate.precast_fp32_weight = True
+        else:
+            self.gate = _Gate(config.hidden_size, config.n_routed_experts)
+        eplb = getattr(parallel_config, "eplb_config", None)
+        self.enable_eplb = getattr(parallel_config, "enable_eplb", False)
+        self.n_redundant_experts = getattr(eplb, "num_redundant_experts", 0) if eplb is not None else 0
+        self.n_logical_experts = self.n_routed_experts
+        self.n_physical_experts = self.n_logical_experts + self.n_redundant_experts
+        self.ep_size = 1
+        self.n_local_physical_experts = self.n_physical_experts
+        self.physical_expert_start = 0
+        self.physical_expert_end = self.n_local_physical_experts
+        if config.n_shared_experts is None or v4 is None:
+            self.shared_experts = None
+        else:
+            self.shared_experts = v4.DeepseekV2MLP(
+                hidden_size=config.hidden_size,
+                intermediate_size=config.moe_intermediate_size * config.n_shared_experts,
+                hidden_act=config.hidden_act, swiglu_limit=self.swiglu_limit, quant_config=quant_config,
+                is_sequence_parallel=self.is_sequence_parallel, reduce_results=False,
+                prefix=f"{prefix}.shared_experts")
+        self.hash = self.layer_idx < getattr(config, "num_hash_layers", 0) and not is_draft_layer
+        if self.hash:
+            self.gate.tid2eid = nn.Parameter(
+                torch.zeros(config.vocab_size, config.num_experts_per_tok, dtype=torch.int32), requires_grad=False)
+            self.gate.e_score_correction_bias = None
+        else:
+            self.gate.tid2eid = None
+            self.gate.e_score_correction_bias = nn.Parameter(
+                torch.zeros(config.n_routed_experts, dtype=torch.float32))
+        self.engine = get_engine()
+        self.experts = _ExpertsFacade(self)
+
+    # -- routing (reference math, torch on the device) -----------------------
+    def _route(self, hs: torch.Tensor, input_ids):
+        """``noaux_tc`` + score function routing: biased scores choose, unbiased
+        scores weigh, renormalise, scale (``deepseek_v4.py:118-148``)."""
+        gating = F.linear(hs.float(), self.gate.weight)
+        if self.scoring_func == "softmax":
+            scores = gating.softmax(dim=-1)
+        elif self.scoring_func == "sigmoid":
+            scores = gating.sigmoid()
+        else:  # sqrtsoftplus
+            scores = F.softplus(gating).sqrt()
+        if self.hash:
+            if input_ids is None:
+                raise RuntimeError("hash-layer routing needs input_ids (forward_context.input_ids is missing)")
+            indices = self.gate.tid2eid[input_ids.to(torch.long).flatten()]
+        else:
+            bias = self.gate.e_score_correction_bias
+            choice = scores if bias is None else scores + bias.to(scores.dtype)
+            indices = torch.topk(choice, k=self.topk, dim=-1, sorted=False)[1]
+        weights = scores.gather(1, indices.to(torch.long))
+        if self.renormalize:
+            weights = weights / weights.sum(dim=-1, keepdim=True)
+        weights = weights * self.routed_scaling_factor
+        return weights, indices
+
+    # -- experts ---------------------------------------------------------------
+    def _expert_table(self, indices: torch.Tensor, device):
+        """Device pointer table of the routed experts and the intermediate size."""
+        eng = self.engine
+        E = self.n_routed_experts
+        ids = indices.detach().to("cpu").numpy()
+        if hasattr(eng, "acquire_table"):
+            table, _ = eng.acquire_table(self.layer_idx, ids, E)
+            inter = eng.bank._layout.shapes["w1p"][0]
+            return table, inter
+        packed = {int(e): eng.get_packed(self.layer_idx, int(e)) for e in np.unique(ids)}
+        inter = next(iter(packed.values()))["w1p"].shape[0]
+        return _ops.expert_table(packed, E, device), inter
+
+    def _run_experts(self, hs, weights, indices, profile):
+        T, D = hs.shape
+        x = hs if (hs.dtype == torch.bfloat16 and hs.is_contiguous()) else hs.to(torch.bfloat16).contiguous()
+        if T == 0:
+            return torch.zeros_like(hs)
+        table, inter = self._expert_table(indices, hs.device)
+        limit = self.swiglu_limit if (self.swiglu_limit and self.swiglu_limit > 0) else 0.0
+        y = _runner(hs.device, self.n_routed_experts, D, inter).forward(
+            x, indices, weights, table, profile=profile, rule=_RULES[_MX_RULE], swiglu_limit=limit)
+        return y.type_as(hs)
+
+    def _routed(self, hs: torch.Tensor, input_ids=None) -> torch.Tensor:
+        """Routed-expert output ``[T, D]`` (``deepseek_v4.py:150-197``); the a4w4
+        profile when the module toggle ``_MXFP4_GMM`` is set (``:199-245``)."""
+        weights, indices = self._route(hs, input_ids)
+        profile = _lib.PROFILE_A4W4 if _MXFP4_GMM else _lib.PROFILE_BF16
+        return self._run_experts(hs, weights, indices, profile)
+
+    def _routed_mxfp4(self, s_w, row, active, group_list, T, hs):
+        """a4w4 path from the reference's sorted view (``deepseek_v4.py:199``
+        signature): each sorted row is one (token, expert) pair; the grouped
+        GEMMs run on the gathered rows and ``moe_unpermute`` sums them back."""
+        experts = torch.repeat_interleave(active.to(torch.int64), group_list.to(hs.device))
+        xs = _ops.moe_permute(hs.to(torch.bfloat16).contiguous(), row.to(torch.int32))
+        out = self._run_experts(xs, s_w.view(-1, 1).float(), experts.view(-1, 1), _lib.PROFILE_A4W4)
+        return _ops.moe_unpermute(out.to(torch.bfloat16).contiguous(), row.to(torch.int32), T).type_as(hs)
+
+    def forward(self, hidden_states: torch.Tensor, input_ids=None) -> torch.Tensor:
+        num_tokens, hidden_dim = hidden_states.shape
+        hs = hidden_states.view(-1, hidden_dim)
+        if self.hash and input_ids is None:
+            from vllm.forward_context import get_forward_context
+            input_ids = getattr(get_forward_context(), "input_ids", None)
+        if self.is_sequence_parallel:
+            hs = v4.sequence_parallel_chunk(hs)
+            if input_ids is not None:
+                input_ids = v4.sequence_parallel_chunk(input_ids)
+        out = self._routed(hs, input_ids)
+        if self.shared_experts is not None:
+            out = out + self.shared_experts(hs)
+        if self.is_sequence_parallel:
+            out = v4.tensor_model_parallel_all_gather(out, 0)[:num_tokens]
+        return out.view(num_tokens, hidden_dim)
+
+
+def _offload_load_weights(self, weights):
+    """Tee of the weight stream: main-model routed experts go to the engine's
+    host pool, everything else to the wrapped ``load_weights``
+    (``deepseek_v4.py:272-288``)."""
+    engine = get_engine()
+    it = iter(weights)
+
+    def filtered():
+        for name, w in it:
+            if is_expert_weight(name):
+                engine.capture(name, w)
+            else:
+                yield name, w
+
+    return _ORIG_LOAD_WEIGHTS(self, filtered())
+
+
+def _causal_lm_class():
+    if v4 is None:
+        return None
+    for name in ("AscendDeepseekV4ForCausalLM", "DeepseekV4ForCausalLM"):
+        cls = getattr(v4, name, None)
+        if cls is not None:
+            return cls
+    return None
+
+
+_LM_CLASS = _causal_lm_class()
+_ORIG_LOAD_WEIGHTS = _LM_CLASS.load_weights if _LM_CLASS is not None else None
+
+
+def install_patches():
+    """Swap in the offload MoE and the load_weights tee (idempotent)."""
+    global _PATCHED
+    if _PATCHED:
+        return
+    if v4 is not None and _LM_CLASS is not None and not getattr(v4, "_DSV4_OFFLOAD_PATCHED", False):
+        v4.DeepseekV4MoE = OffloadDeepseekV4MoE
+        _LM_CLASS.load_weights = _offload_load_weights
+        v4._DSV4_OFFLOAD_PATCHED = True
+    _PATCHED = True

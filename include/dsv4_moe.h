@@ -151,6 +151,51 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
                            const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
                            float swiglu_limit, void* workspace, int64_t workspace_bytes, void* y, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Expert slot cache (replaces ExpertBank's device caches, offload.py:22-151).
+ * One device slot pool (caller-allocated, n_slots * record_bytes, 256-byte
+ * aligned) + pinned host records (one per registered (layer, expert), the
+ * expert's six packed tensors at fixed offsets) + a side copy stream.
+ * ------------------------------------------------------------------------ */
+typedef struct dsv4_slots dsv4_slots;
+
+/* Pure LRU over `capacity` slots, host only (the policy of offload.py:86-100:
+ * hit -> most recent, miss -> free slot or evict least recent; capacity 0
+ * never caches). *hit = 1/0; *evicted = evicted key or -1. */
+int dsv4_lru_create(int capacity, void** out);
+int dsv4_lru_destroy(void* lru);
+int dsv4_lru_access(void* lru, int64_t key, int* hit, int* slot, int64_t* evicted);
+int dsv4_lru_keys(void* lru, int64_t* out, int max, int* n); /* least -> most recent */
+
+/* pin_host: allocate host records page-locked (hipHostMalloc); on failure the
+ * manager degrades to pageable memory, as ExpertBank.register does
+ * (offload.py:62-67). */
+int dsv4_slots_create(int device, int64_t record_bytes, int n_slots, void* device_pool, int pin_host,
+                      dsv4_slots** out);
+int dsv4_slots_destroy(dsv4_slots* s);
+/* Host record of (layer, eid); create=1 allocates it (ExpertBank.register,
+ * offload.py:59-68). *pinned tells whether it is page-locked. */
+int dsv4_slots_host_record(dsv4_slots* s, int layer, int eid, int create, void** record, int* pinned);
+int dsv4_slots_num_registered(dsv4_slots* s, int64_t* n);
+/* Makes the n experts of `layer` resident and returns their slots (the batched
+ * form of ExpertBank.get_packed, offload.py:103-129). Misses are copied on the
+ * side copy stream; `compute_stream` waits for the copies the returned slots
+ * depend on. Slots returned by the previous acquire are released first (their
+ * readers are the work enqueued on compute_stream before this call). */
+int dsv4_slots_acquire(dsv4_slots* s, int layer, const int32_t* eids, int n, void* compute_stream,
+                       int32_t* slots, int* n_miss);
+/* Starts copies for the non-resident experts of a later batch (no waits). */
+int dsv4_slots_prefetch(dsv4_slots* s, int layer, const int32_t* eids, int n, int* n_issued);
+int dsv4_slots_release(dsv4_slots* s, void* compute_stream);
+int dsv4_slots_copy_record(dsv4_slots* s, int layer, int eid, void* dst, void* stream);
+int dsv4_slots_lookup(dsv4_slots* s, int layer, int eid, int32_t* slot);
+int dsv4_slots_keys(dsv4_slots* s, int64_t* out, int max, int* n);
+int dsv4_slots_sync(dsv4_slots* s);
+int dsv4_slots_invalidate(dsv4_slots* s);
+/* stats[9] = hits, misses, evictions, prefetched, bytes_h2d, copies, cached, capacity, pinned */
+int dsv4_slots_stats(dsv4_slots* s, int64_t* stats);
+int dsv4_slots_reset_stats(dsv4_slots* s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,286 @@
+"""GPU tests of the reference-shaped surface: npu_ops, offload.ExpertBank and
+the plugin's OffloadDeepseekV4MoE, against the oracle."""
+
+import types
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+import npu_ops
+from offload import ExpertBank
+import dsv4_plugin.models.deepseek_v4 as mod
+from dsv4_plugin.core.engine import ExpertOffloadEngine
+from oracle import mxfp4 as Q
+from oracle import moe as M
+from oracle import routing as RT
+from dsv4_hip import synth
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _bf(bits, dev):
+    return torch.from_numpy(np.ascontiguousarray(bits, np.uint16).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def rel(a, b):
+    return float(np.abs(np.asarray(a, np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+# ---------------------------------------------------------------- npu_ops
+def test_npu_ops_dequant_reference_vector(gpu):
+    # test_npu_ops.py:185-195: int8 packed + e8m0 scales, N=8, K/2=128, scales 120..133
+    rng = np.random.default_rng(0)
+    packed = rng.integers(0, 256, (8, 128), dtype=np.uint8)
+    sb = rng.integers(120, 134, (8, 8), dtype=np.uint8)
+    wp = torch.from_numpy(packed).view(torch.int8).to(gpu)
+    sc = torch.from_numpy(sb).view(torch.float8_e8m0fnu).to(gpu)
+    out = npu_ops.dequant_fp4_weight(wp, sc)
+    assert out.dtype == torch.bfloat16 and out.shape == (8, 256)
+    assert np.array_equal(_bits(out), Q.dequant_fp4_weight(packed, sb))
+    out32 = npu_ops.dequant_fp4_weight(wp, sc, torch.float32)
+    assert np.array_equal(out32.cpu().numpy(), Q.dequant_fp4_weight_f32(packed, sb))
+
+
+def test_npu_ops_e8m0_to_fp32(gpu):
+    b = torch.arange(256, dtype=torch.int32).to(torch.uint8)
+    got = npu_ops.e8m0_to_fp32(b.to(gpu)).cpu()
+    ref = torch.pow(2.0, b.int().float() - 127.0)
+    assert torch.equal(got, ref)
+    got2 = npu_ops.e8m0_to_fp32(b.view(torch.float8_e8m0fnu).to(gpu)).cpu()
+    assert torch.equal(got2, ref)
+
+
+def test_npu_ops_act_quant_both_forms(gpu):
+    torch.manual_seed(0)
+    x = (torch.randn(64, 512) * 3).to(torch.bfloat16)
+    xb = x.view(torch.int16).numpy().view(np.uint16)
+    rt, codes, s, _ = Q.act_quant(xb, 128)
+    xd = x.to(gpu)
+    out = npu_ops.act_quant(xd, 128, "ue8m0", None, True)
+    assert out is xd and np.array_equal(_bits(out), rt)
+    y, sc = npu_ops.act_quant(x.to(gpu), 128, "ue8m0", None, False)
+    assert y.dtype == torch.float8_e4m3fn
+    assert np.array_equal(y.cpu().view(torch.uint8).numpy(), codes)
+    assert np.array_equal(sc.cpu().numpy(), s)
+    # a non-contiguous input is written back in place
+    big = x.to(gpu).repeat(1, 2)[:, :512]
+    npu_ops.act_quant(big, 128, "ue8m0", None, True)
+    assert np.array_equal(_bits(big), rt)
+
+
+def test_npu_ops_fp4_act_quant_and_dynamic_mx_quant(gpu):
+    torch.manual_seed(1)
+    x2 = (torch.randn(64, 256) * 2).to(torch.bfloat16)
+    xb = x2.view(torch.int16).numpy().view(np.uint16)
+    dq, packed, sc = Q.fp4_act_quant(xb, 32)
+    xd = x2.to(gpu)
+    assert npu_ops.fp4_act_quant(xd, 32, True) is xd
+    assert np.array_equal(_bits(xd), dq)
+    with pytest.raises(NotImplementedError):
+        npu_ops.fp4_act_quant(x2.to(gpu), 32, False)
+    for rule in ("ceil_div6", "ocp_floor"):
+        _, p_ref, s_ref = Q.dynamic_mx_quant(xb, rule)
+        p, s = npu_ops.dynamic_mx_quant(x2.to(gpu), rule)
+        assert np.array_equal(p.cpu().numpy(), p_ref) and np.array_equal(s.cpu().numpy(), s_ref)
+
+
+def test_npu_ops_align_permute_unpermute(gpu):
+    T, K, E = 32, 8, 256
+    ids = synth.zipf_topk(T, K, E)
+    w = synth.routing_weights(T, K)
+    al = RT.moe_align(ids, w, E, 16)
+    res = npu_ops.moe_align(torch.from_numpy(ids).to(gpu), torch.from_numpy(w).to(gpu), E)
+    assert np.array_equal(res.order.cpu().numpy(), al["order"])
+    assert np.array_equal(res.active_list().cpu().numpy(), al["active"])
+    x = synth.bf16_normal(np.random.default_rng(1), (T, 512)).to(gpu)
+    xs = npu_ops.moe_permute(x, res.row)
+    assert torch.equal(xs.cpu(), x.cpu()[torch.from_numpy(al["row"])])
+    y = npu_ops.moe_unpermute(xs, res.row, T)
+    want = RT.unpermute(_bits(xs), al["row"], T)
+    assert np.array_equal(_bits(y), want)
+
+
+@pytest.mark.parametrize("form", ["a4w4_list", "a4w4_stacked_view", "bf16_x"])
+def test_npu_ops_grouped_matmul_groups_2_0_3(gpu, form):
+    # _bench_gmm.py:8-22 group pattern, MXFP4 weights [N, K/2]
+    counts, N, Kd = [2, 0, 3], 256, 512
+    rng = np.random.default_rng(3)
+    wts = [synth.packed_weight(rng, N, Kd) for _ in counts]
+    x = synth.bf16_normal(rng, (5, Kd))
+    xb = x.view(torch.int16).numpy().view(np.uint16)
+    if form == "bf16_x":
+        rt = Q.act_quant(xb, 128)[0]
+        a_f = Q.bf16_bits_to_f32(rt)
+        out = npu_ops.grouped_matmul(x=[x.to(gpu)], weight=[torch.from_numpy(w).to(gpu) for w, _ in wts],
+                                     scale=[torch.from_numpy(s).to(gpu) for _, s in wts], group_list=counts)
+    else:
+        _, xp, xs = Q.ocp_mx_quant(xb, 32)
+        a_f = Q.fp4_codes_to_f32(xp, xs)
+        if form == "a4w4_list":
+            weight = [torch.from_numpy(w).to(gpu) for w, _ in wts]
+            scale = [torch.from_numpy(s).to(gpu) for _, s in wts]
+        else:  # the reference's stacked, transposed views (deepseek_v4.py:220-223)
+            weight = [torch.stack([torch.from_numpy(w) for w, _ in wts]).to(gpu).transpose(1, 2)]
+            scale = [torch.stack([torch.from_numpy(s).reshape(N, Kd // 64, 2) for _, s in wts]).to(gpu)
+                     .transpose(1, 2)]
+        out = npu_ops.grouped_matmul(x=[torch.from_numpy(xp).to(gpu)], weight=weight, scale=scale,
+                                     per_token_scale=[torch.from_numpy(xs).to(gpu).reshape(5, Kd // 64, 2)],
+                                     group_list=torch.tensor(counts, device=gpu), group_list_type=1)
+    got = Q.bf16_bits_to_f32(_bits(out))
+    o = 0
+    for (w, s), c in zip(wts, counts):
+        if c:
+            ref = M.matmul_nt(a_f[o:o + c], Q.dequant_fp4_weight_f32(w, s))
+            assert rel(got[o:o + c], ref) <= (2e-2 if form != "bf16_x" else 1e-2)
+        o += c
+
+
+# ---------------------------------------------------------------- ExpertBank
+def make_expert(seed, N1=64, K1=64, N2=64, K2=64):
+    """test_offload.py:11-20: random packed experts in the checkpoint layout."""
+    g = torch.Generator().manual_seed(seed)
+
+    def packed(N, K):
+        return torch.randint(0, 256, (N, K // 2), dtype=torch.uint8, generator=g)
+
+    def scale(N, K):
+        return torch.randint(100, 150, (N, K // 32), dtype=torch.uint8, generator=g)
+    return (packed(N1, K1), scale(N1, K1), packed(N2, K2), scale(N2, K2), packed(N1, K1), scale(N1, K1))
+
+
+def test_expert_bank_get_and_lru_known_answer(gpu):
+    # test_offload.py:22-86 on the device bank
+    bank = ExpertBank(capacity=4, device="npu:0", dtype=torch.bfloat16)
+    refs = {}
+    for eid in range(5):
+        t = make_expert(100 + eid)
+        bank.register(0, eid, *t)
+        refs[(0, eid)] = t
+    for eid in range(3):
+        t = make_expert(200 + eid)
+        bank.register(1, eid, *t)
+        refs[(1, eid)] = t
+    assert bank.num_experts() == 8 and bank.has(0, 4) and bank.has(1, 2) and not bank.has(0, 5)
+    d = bank.get(0, 0)
+    wp, ws = refs[(0, 0)][0], refs[(0, 0)][1]
+    assert np.array_equal(_bits(d["w1"]), Q.dequant_fp4_weight(wp.numpy(), ws.numpy()))
+    assert tuple(d["w2"].shape) == (64, 64)
+    h0 = bank.hits
+    bank.get(0, 0)
+    assert bank.hits == h0 + 1
+    bank.invalidate()
+    bank.hits = bank.misses = bank.evictions = 0
+    for eid in range(4):
+        bank.get(0, eid)
+    assert len(bank._cache) == 4
+    bank.get(0, 0)
+    bank.get(1, 0)
+    assert (0, 1) not in bank._cache and (0, 0) in bank._cache and (1, 0) in bank._cache
+    assert bank.evictions == 1
+    s = bank.stats()
+    assert s["misses"] == 5 and s["hits"] == 1 and s["hit_rate"] == 1 / 6
+    bank0 = ExpertBank(capacity=0, device="cuda:0")
+    bank0.register(0, 0, *make_expert(7))
+    bank0.get(0, 0)
+    bank0.get(0, 0)
+    assert len(bank0._cache) == 0 and bank0.stats()["misses"] == 2
+
+
+def test_packed_slots_survive_eviction_pressure(gpu, monkeypatch):
+    # 40 experts through 8 packed slots; every slot read is queued on the stream
+    # before the next acquire may evict it; all reads are checked at the end.
+    monkeypatch.setenv("DSV4_PACKED_SLOTS", "8")
+    bank = ExpertBank(capacity=2, device="cuda:0")
+    refs = {}
+    for e in range(40):
+        refs[e] = make_expert(500 + e, 128, 512, 512, 128)
+        bank.register(3, e, *refs[e])
+    rng = np.random.default_rng(0)
+    outs = []
+    for it in range(60):
+        for e in rng.choice(40, size=3, replace=False):
+            p = bank.get_packed(3, int(e))
+            outs.append((int(e), npu_ops.dequant_fp4_weight(p["w2p"], p["w2s"])))
+    torch.cuda.synchronize()
+    for e, o in outs:
+        assert np.array_equal(_bits(o), Q.dequant_fp4_weight(refs[e][2].numpy(), refs[e][3].numpy())), e
+    s = bank.stats()
+    assert s["packed_misses"] + s["packed_hits"] == 180 and s["packed_evictions"] > 0
+    assert s["packed_cached"] == 8 and s["h2d_bytes"] == s["packed_misses"] * bank._layout.record_bytes
+
+
+# ---------------------------------------------------------------- plugin layer
+def _make_plugin(engine, E, K, layer=3, is_hash=False, D=1024):
+    """test_moe_align.py:98-119: build via __new__ and set the fields by hand."""
+    m = mod.OffloadDeepseekV4MoE.__new__(mod.OffloadDeepseekV4MoE)
+    nn.Module.__init__(m)
+    m.hash = is_hash
+    m.topk = K
+    m.renormalize = True
+    m.scoring_func = "sqrtsoftplus"
+    m.routed_scaling_factor = 1.5
+    m.swiglu_limit = 10.0
+    m.n_routed_experts = E
+    m.is_sequence_parallel = False
+    m.shared_experts = None
+    m.layer_idx = layer
+    m.engine = engine
+    g = torch.Generator().manual_seed(layer)
+    m.gate = types.SimpleNamespace(
+        weight=(torch.randn(E, D, generator=g) * 0.05).to("cuda:0"),
+        e_score_correction_bias=None if is_hash else (torch.randn(E, generator=g) * 0.01).to("cuda:0"),
+        tid2eid=torch.randint(0, E, (100, K), generator=g).to("cuda:0") if is_hash else None)
+    return m
+
+
+@pytest.mark.parametrize("fast", [True, False])
+@pytest.mark.parametrize("is_hash", [False, True])
+def test_plugin_routed_matches_oracle(gpu, fast, is_hash):
+    E, K, D, I, T, layer = 32, 6, 1024, 512, 8, 3
+    engine = ExpertOffloadEngine(slot_capacity=16, device="cuda:0")
+    host = {}
+    for e in range(E):
+        host[e] = synth.expert_weights(e, D, I)
+        for w in ("w1", "w2", "w3"):
+            engine.capture(f"layers.{layer}.ffn.experts.{e}.{w}.weight", torch.from_numpy(host[e][w + "p"]).view(torch.int8))
+            engine.capture(f"layers.{layer}.ffn.experts.{e}.{w}.scale",
+                           torch.from_numpy(host[e][w + "s"]).view(torch.float8_e8m0fnu))
+    assert engine.captured == E
+    eng_obj = engine if fast else types.SimpleNamespace(get=engine.get, get_packed=engine.get_packed)
+    m = _make_plugin(eng_obj, E, K, layer, is_hash, D)
+    x = (synth.bf16_normal(np.random.default_rng(5), (T, D)).float() * 0.5).to(torch.bfloat16).to(gpu)
+    ids = torch.randint(0, 100, (T,), generator=torch.Generator().manual_seed(2)).to(gpu)
+    w, idx = m._route(x, ids)
+    xb = _bits(x)
+    ref_b = M.routed_bf16(xb, idx.cpu().numpy(), w.cpu().numpy(), host, n_experts=E)
+    y = m._routed(x, ids)
+    torch.cuda.synchronize()
+    assert rel(Q.bf16_bits_to_f32(_bits(y)), Q.bf16_bits_to_f32(ref_b["y"])) <= 1e-2
+    saved = mod._MXFP4_GMM
+    mod._MXFP4_GMM = True
+    try:
+        y4 = m._routed(x, ids)
+    finally:
+        mod._MXFP4_GMM = saved
+    ref_a = M.routed_a4w4(xb, idx.cpu().numpy(), w.cpu().numpy(), host, n_experts=E, rule="ocp_floor")
+    assert rel(Q.bf16_bits_to_f32(_bits(y4)), Q.bf16_bits_to_f32(ref_a["y"])) <= 2e-2
+    # test_moe_align.py:180-188 dual threshold between the two profiles (relative to the output scale)
+    d = np.abs(Q.bf16_bits_to_f32(_bits(y4)) - Q.bf16_bits_to_f32(_bits(y)))
+    scale = np.abs(Q.bf16_bits_to_f32(_bits(y))).max()
+    assert d.max() < 0.35 * scale and d.mean() < 0.08 * scale
+    # the reference-internal a4w4 entry (sorted view) gives the same result
+    al = RT.moe_align(idx.cpu().numpy(), w.cpu().numpy(), E, 16)
+    y4b = m._routed_mxfp4(torch.from_numpy(al["s_w"]).to(gpu), torch.from_numpy(al["row"]).to(gpu),
+                          torch.from_numpy(al["active"]).to(gpu), torch.from_numpy(al["group_list"]).to(gpu),
+                          T, x)
+    torch.cuda.synchronize()
+    assert rel(Q.bf16_bits_to_f32(_bits(y4b)), Q.bf16_bits_to_f32(ref_a["y"])) <= 2e-2
+    if fast:
+        s = engine.stats()
+        assert s["packed_hits"] + s["packed_misses"] >= len(np.unique(idx.cpu().numpy()))
