@@ -47,6 +47,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default="", help="profile helper: run only 'decode', 'dequant' or 'prefill'")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="first copy 1 GiB device-to-device (a plain copy of known size for counter calibration)")
     return ap.parse_args()
 
 
@@ -100,47 +102,53 @@ def time_layer(runner, batches_dev, tables, steps, warmup, profile, rule):
 
 
 def measure_gemms(batches_dev, batches_host, tables, steps, profile, rule):
-    """Average gate/up and down GEMM durations (HIP events) and algorithmic bytes/flops."""
+    """Average gate/up and down GEMM durations and their algorithmic bytes.
+
+    The operands of every step (layout, quantised x, quantised h) are prepared
+    first; then each GEMM is launched back to back over all steps between two
+    HIP events on the stream the kernels run on, so the host never leaves the
+    GPU idle inside the timed window."""
     from dsv4_hip import ops, AFMT_E4M3, AFMT_E2M1, PROFILE_BF16
     n, L = len(batches_dev), len(tables)
-    t_gu, t_dn, b_gu, b_dn, flops = [], [], [], [], []
-    s = torch.cuda.current_stream()
+    fp8 = profile == PROFILE_BF16
+    afmt = AFMT_E4M3 if fp8 else AFMT_E2M1
+    prep, b_gu, b_dn, flops = [], [], [], []
     for i in range(steps):
         x, ids, w = batches_dev[i % n]
         T, K = ids.shape
         A = len(np.unique(batches_host[i % n][1]))
         al = ops.moe_align(ids, None, E)
-        fp8 = profile == PROFILE_BF16
         if fp8:
             q = ops.fp8_act_quant(x, 128, want_codes=True, want_e8m0x4=True)
-            a, a_s, afmt = q["codes"], q["e8m0x4"], AFMT_E4M3
+            a, a_s = q["codes"], q["e8m0x4"]
         else:
             a, a_s, _ = ops.mxfp4_act_quant(x, rule)
-            afmt = AFMT_E2M1
-        e0, e1, e2, e3 = (torch.cuda.Event(enable_timing=True) for _ in range(4))
-        e0.record(s)
         h = ops.gemm_gateup(afmt, a, a_s, K, al, tables[i % L], D, I, w.reshape(-1), 10.0)
-        e1.record(s)
         if fp8:
             q = ops.fp8_act_quant(h, 128, want_codes=True, want_e8m0x4=True)
             ha, has = q["codes"], q["e8m0x4"]
         else:
             ha, has, _ = ops.mxfp4_act_quant(h, rule)
-        e2.record(s)
-        ops.gemm_down(afmt, ha, has, al, tables[i % L], I, D)
-        e3.record(s)
-        e3.synchronize()
-        t_gu.append(e0.elapsed_time(e1) * 1e-3)
-        t_dn.append(e2.elapsed_time(e3) * 1e-3)
+        prep.append((a, a_s, K, al, tables[i % L], w.reshape(-1), ha, has))
         R = T * K
         a_bytes = T * D * (1 if fp8 else 0.5) + T * D / 32
         b_gu.append(A * GATEUP_BYTES + a_bytes + 2 * R * I)
         b_dn.append(A * (EXPERT_BYTES - GATEUP_BYTES) + R * I * ((1 if fp8 else 0.5) + 1 / 32) + 2 * R * D)
         flops.append(6.0 * R * D * I)
-    k = max(1, steps // 5)  # drop the first fifth (warm-up)
-    return {"t_gateup": float(np.mean(t_gu[k:])), "t_down": float(np.mean(t_dn[k:])),
-            "bytes_gateup": float(np.mean(b_gu[k:])), "bytes_down": float(np.mean(b_dn[k:])),
-            "flops": float(np.mean(flops[k:]))}
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    e0.record(s)
+    for a, a_s, K, al, tab, wf, _, _ in prep:
+        ops.gemm_gateup(afmt, a, a_s, K, al, tab, D, I, wf, 10.0)
+    e1.record(s)
+    for _, _, _, al, tab, _, ha, has in prep:
+        ops.gemm_down(afmt, ha, has, al, tab, I, D)
+    e2.record(s)
+    e2.synchronize()
+    return {"t_gateup": e0.elapsed_time(e1) * 1e-3 / steps, "t_down": e1.elapsed_time(e2) * 1e-3 / steps,
+            "bytes_gateup": float(np.mean(b_gu)), "bytes_down": float(np.mean(b_dn)),
+            "flops": float(np.mean(flops))}
 
 
 def measure_dequant(dev, gen, n_mats=64, reps=5):
@@ -196,6 +204,14 @@ def main():
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
     T, K = 8, 8
+    if args.calib_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"calib-copy: {src.numel()} bytes read, {dst.numel()} bytes written", file=sys.stderr)
+        del src, dst
+        torch.cuda.empty_cache()
     if args.only in ("", "decode"):
         pools, tables = gen_layer_weights(dev, args.layers, gen)
         host = routing_batches(64, T, K, 11)
@@ -205,6 +221,14 @@ def main():
         s = time_layer(runner, dev_b, tables, args.steps, args.warmup, PROFILE_BF16, RULE_OCP_FLOOR)
         gm = measure_gemms(dev_b, host, tables, min(args.steps, 100), PROFILE_BF16, RULE_OCP_FLOOR)
         ach = gm["bytes_gateup"] / gm["t_gateup"] / 1e9
+        # HBM bytes per launch from the committed counter profile (FETCH_SIZE/WRITE_SIZE
+        # scaled by a 1 GiB copy): measured traffic / algorithmic bytes, applied to this run
+        traffic = None
+        tpath = os.path.join(ROOT, "profiles", "moe_gemm_decode_bf16_traffic.json")
+        if os.path.exists(tpath):
+            with open(tpath) as f:
+                tr = json.load(f)
+            traffic = tr["gateup_traffic_over_algorithmic"] * gm["bytes_gateup"]
         line = {
             "metric": "MoE decode tok/s (bf16 profile, 256 experts top-8, hidden 4096, inter 2048)",
             "value": T / s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -215,7 +239,8 @@ def main():
                        "tokens": T, "topk": K, "experts": E, "hidden": D, "inter": I,
                        "weight_sets_cycled": args.layers},
             "roofline": {"bound": "hbm", "kernel": "moe_gemm_kernel<E4M3, gate/up>", "achieved": ach,
-                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": ach / HBM_PEAK_GBS, "traffic": None,
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": ach / HBM_PEAK_GBS, "traffic": traffic,
+                         "traffic_source": "profiles/moe_gemm_decode_bf16_traffic.json" if traffic else None,
                          "algorithmic_bytes_per_launch": gm["bytes_gateup"],
                          "avg_launch_us": gm["t_gateup"] * 1e6},
             "gemm": {"gateup_us": gm["t_gateup"] * 1e6, "down_us": gm["t_down"] * 1e6,

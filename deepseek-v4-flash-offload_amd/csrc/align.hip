@@ -5,24 +5,24 @@
 // padded block layout used by the grouped GEMM: each expert's rows are padded
 // to a multiple of block_m so that an M block never straddles two experts.
 //
-// One workgroup of 1024 threads:
+// One workgroup (256 threads for decode-sized inputs, 1024 otherwise):
 //   1. LDS histogram (atomic increments; counts are order-independent).
 //   2. Three block-wide exclusive scans: unpadded offsets, padded offsets,
 //      active-expert ranks.
-//   3. Stable scatter in chunks of 1024 entries: within a wave, entries with
-//      the same expert are found by a ballot match over the key bits; the rank
-//      is the popcount of lower lanes; per-wave counts go through LDS to rank
-//      across the 16 waves; a running count per expert carries across chunks.
+//   3. Stable scatter in chunks of one entry per thread: within a wave,
+//      entries with the same expert are found by a ballot match over the key
+//      bits; the rank is the popcount of lower lanes; per-wave counts go
+//      through LDS to rank across the waves; a running count per expert
+//      carries across chunks.
 #include "common.h"
 #include "kernels.h"
 
 namespace {
 
-constexpr int kThreads = 1024;
-constexpr int kWaves = kThreads / 64;
-
-// exclusive scan of one int per thread across the workgroup; returns the total.
+// exclusive scan of one int per thread across the NT-thread workgroup; returns the total.
+template <int NT>
 __device__ int block_exclusive_scan(int v, int* lds_waves, int* out_total) {
+  constexpr int kWaves = NT / 64;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int incl = v;
   for (int o = 1; o < 64; o <<= 1) {
@@ -47,11 +47,13 @@ __device__ int block_exclusive_scan(int v, int* lds_waves, int* out_total) {
   return r;
 }
 
-template <typename IdT>
-__global__ __launch_bounds__(kThreads) void moe_align_kernel(const IdT* __restrict__ ids,
-                                                             const float* __restrict__ topk_w, int R, int K,
-                                                             int E, int block_m, int max_blocks,
-                                                             Dsv4AlignOut o) {
+template <typename IdT, int NT>
+__global__ __launch_bounds__(NT) void moe_align_kernel(const IdT* __restrict__ ids,
+                                                       const float* __restrict__ topk_w, int R, int K,
+                                                       int E, int block_m, int max_blocks,
+                                                       Dsv4AlignOut o) {
+  constexpr int kThreads = NT;
+  constexpr int kWaves = NT / 64;
   extern __shared__ int lds[];
   int* cnt = lds;                    // [E + 1] (slot E collects out-of-range ids)
   int* off_u = cnt + (E + 1);        // [E]
@@ -79,9 +81,9 @@ __global__ __launch_bounds__(kThreads) void moe_align_kernel(const IdT* __restri
   // 2. scans over experts (E <= kThreads)
   const int c = (tid < E) ? cnt[tid] : 0;
   const int padded = ((c + block_m - 1) / block_m) * block_m;
-  const int ou = block_exclusive_scan(c, scan_tmp, &totals[0]);
-  const int op = block_exclusive_scan(padded, scan_tmp, &totals[1]);
-  const int oa = block_exclusive_scan(c > 0 ? 1 : 0, scan_tmp, &totals[2]);
+  const int ou = block_exclusive_scan<NT>(c, scan_tmp, &totals[0]);
+  const int op = block_exclusive_scan<NT>(padded, scan_tmp, &totals[1]);
+  const int oa = block_exclusive_scan<NT>(c > 0 ? 1 : 0, scan_tmp, &totals[2]);
   if (tid < E) {
     off_u[tid] = ou;
     off_p[tid] = op;
@@ -152,12 +154,25 @@ __global__ __launch_bounds__(kThreads) void moe_align_kernel(const IdT* __restri
 
 hipError_t launch_moe_align(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K, int E,
                             int block_m, int max_blocks, const Dsv4AlignOut& o, hipStream_t st) {
-  const size_t lds = sizeof(int) * (size_t)((E + 1) + E + E + (E + 1) + kWaves * (E + 1));
-  if (ids_int64)
-    hipLaunchKernelGGL(moe_align_kernel<long long>, dim3(1), dim3(kThreads), lds, st,
-                       (const long long*)topk_ids, topk_w, R, K, E, block_m, max_blocks, o);
-  else
-    hipLaunchKernelGGL(moe_align_kernel<int32_t>, dim3(1), dim3(kThreads), lds, st,
-                       (const int32_t*)topk_ids, topk_w, R, K, E, block_m, max_blocks, o);
+  // small problems (decode) run on 4 waves: fewer waves to synchronise; larger
+  // ones (prefill, or E > 256) on 16 waves: fewer sequential 1024-entry chunks
+  const bool small = E <= 256 && R <= 2048;
+  const int nwaves = small ? 4 : 16;
+  const size_t lds = sizeof(int) * (size_t)((E + 1) + E + E + (E + 1) + nwaves * (E + 1));
+  if (small) {
+    if (ids_int64)
+      hipLaunchKernelGGL((moe_align_kernel<long long, 256>), dim3(1), dim3(256), lds, st,
+                         (const long long*)topk_ids, topk_w, R, K, E, block_m, max_blocks, o);
+    else
+      hipLaunchKernelGGL((moe_align_kernel<int32_t, 256>), dim3(1), dim3(256), lds, st,
+                         (const int32_t*)topk_ids, topk_w, R, K, E, block_m, max_blocks, o);
+  } else {
+    if (ids_int64)
+      hipLaunchKernelGGL((moe_align_kernel<long long, 1024>), dim3(1), dim3(1024), lds, st,
+                         (const long long*)topk_ids, topk_w, R, K, E, block_m, max_blocks, o);
+    else
+      hipLaunchKernelGGL((moe_align_kernel<int32_t, 1024>), dim3(1), dim3(1024), lds, st,
+                         (const int32_t*)topk_ids, topk_w, R, K, E, block_m, max_blocks, o);
+  }
   return hipGetLastError();
 }

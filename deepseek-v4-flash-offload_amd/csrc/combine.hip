@@ -27,7 +27,6 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const u32x4* __restric
   }
 }
 
-constexpr int kMaxK = 32;
 
 DSV4_DEV void accumulate8(float* acc, u32x4 v) {
   acc[0] += dsv4::bf16_to_f32(v.x & 0xffffu); acc[1] += dsv4::bf16_to_f32(v.x >> 16);
@@ -45,28 +44,43 @@ DSV4_DEV u32x4 pack8(const float* acc) {
   return r;
 }
 
+// Order of n <= 64 entries held one per lane (lanes >= n ignored): returns the
+// calling lane's rank under (key, lane) ordering. Registers only - no local
+// arrays, which would be placed in scratch memory.
+DSV4_DEV int wave_rank(long long key, int n) {
+  const int lane = threadIdx.x & 63;
+  int rank = 0;
+  for (int j = 0; j < n; ++j) {
+    const long long kj = __shfl(key, j, 64);
+    rank += (kj < key || (kj == key && j < lane)) ? 1 : 0;
+  }
+  return rank;
+}
+
+// lane holding rank r (uniform result)
+DSV4_DEV int wave_select_rank(int rank, int n, int r) {
+  const int lane = threadIdx.x & 63;
+  return __ffsll((unsigned long long)__ballot(lane < n && rank == r)) - 1;
+}
+
 // Workgroups of 64 lanes tile (token, 512-column chunk); each lane owns 8
-// columns. The token's K entries are ordered by (key, k) with an insertion sort
-// that every lane performs identically.
+// columns. The token's K entries are visited in (expert id, k) order.
 template <typename IdT>
 __global__ __launch_bounds__(64) void combine_flat_kernel(const u32x4* __restrict__ src,
                                                           const IdT* __restrict__ ids, int K, int D,
                                                           u32x4* __restrict__ y) {
   const int t = blockIdx.y;
-  int ord[kMaxK];
-  long long key[kMaxK];
-  for (int k = 0; k < K; ++k) {
-    long long kk = (long long)ids[(int64_t)t * K + k];
-    int j = k;
-    while (j > 0 && key[j - 1] > kk) { key[j] = key[j - 1]; ord[j] = ord[j - 1]; --j; }
-    key[j] = kk; ord[j] = k;
-  }
+  const int lane = threadIdx.x;
+  const long long key = lane < K ? (long long)ids[(int64_t)t * K + lane] : 0;
+  const int rank = wave_rank(key, K);
   const int vecs = D / 8;
-  const int c = blockIdx.x * 64 + threadIdx.x;
-  if (c >= vecs) return;
+  const int c = blockIdx.x * 64 + lane;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j = 0; j < K; ++j) accumulate8(acc, src[((int64_t)t * K + ord[j]) * vecs + c]);
-  y[(int64_t)t * vecs + c] = pack8(acc);
+  for (int r = 0; r < K; ++r) {
+    const int k = wave_select_rank(rank, K, r);
+    if (c < vecs) accumulate8(acc, src[((int64_t)t * K + k) * vecs + c]);
+  }
+  if (c < vecs) y[(int64_t)t * vecs + c] = pack8(acc);
 }
 
 __global__ __launch_bounds__(256) void bucket_rows_kernel(const int32_t* __restrict__ row, int R, int T, int Kmax,
@@ -91,18 +105,19 @@ __global__ __launch_bounds__(256) void combine_rows_kernel(const u32x4* __restri
                                                            u32x4* __restrict__ y) {
   const int t = blockIdx.x;
   const int n = min(cnt[t], Kmax);
-  int p[kMaxK];
-  for (int k = 0; k < n; ++k) {
-    int v = pos[(int64_t)t * Kmax + k];
-    int j = k;
-    while (j > 0 && p[j - 1] > v) { p[j] = p[j - 1]; --j; }
-    p[j] = v;
-  }
+  const int lane = threadIdx.x & 63;
+  // each wave ranks the token's row positions itself (ascending position)
+  const long long mypos = lane < n ? (long long)pos[(int64_t)t * Kmax + lane] : 0;
+  const int rank = wave_rank(mypos, n);
   const int vecs = D / 8;
-  for (int c = threadIdx.x; c < vecs; c += 256) {
+  for (int c0 = 0; c0 < vecs; c0 += 256) {
+    const int c = c0 + threadIdx.x;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < n; ++j) accumulate8(acc, src[(int64_t)p[j] * vecs + c]);
-    y[(int64_t)t * vecs + c] = pack8(acc);
+    for (int r = 0; r < n; ++r) {
+      const long long row = __shfl(mypos, wave_select_rank(rank, n, r), 64);
+      if (c < vecs) accumulate8(acc, src[row * vecs + c]);
+    }
+    if (c < vecs) y[(int64_t)t * vecs + c] = pack8(acc);
   }
 }
 
