@@ -188,8 +188,8 @@ int dsv4_moe_gemm_gateup(int afmt, const void* a, const void* a_scale, int a_row
                          const int32_t* block_expert, const int32_t* num_post_padded, int R, int block_m,
                          int max_blocks, const void* expert_table, int D, int I, const float* topk_w,
                          float swiglu_limit, void* h_out, void* stream) {
-  REQUIRE(block_m == DSV4_GEMM_BLOCK_M, DSV4_ERR_UNSUPPORTED, "gemm: block_m %d unsupported (%d)", block_m,
-          DSV4_GEMM_BLOCK_M);
+  REQUIRE(moe_gemm_supported_block_m(block_m), DSV4_ERR_UNSUPPORTED,
+          "gemm: block_m %d unsupported (16, 64 or 128)", block_m);
   REQUIRE(I > 0 && I % 128 == 0, DSV4_ERR_UNSUPPORTED, "gemm gate/up: I=%d not a multiple of 128", I);
   REQUIRE(a_row_div > 0, DSV4_ERR_SHAPE, "gemm gate/up: a_row_div=%d", a_row_div);
   if (R == 0 || max_blocks == 0) return DSV4_OK;
@@ -207,8 +207,8 @@ int dsv4_moe_gemm_gateup(int afmt, const void* a, const void* a_scale, int a_row
 int dsv4_moe_gemm_down(int afmt, const void* a, const void* a_scale, const int32_t* sorted_ids,
                        const int32_t* block_expert, const int32_t* num_post_padded, int R, int block_m,
                        int max_blocks, const void* expert_table, int I, int D, void* out, void* stream) {
-  REQUIRE(block_m == DSV4_GEMM_BLOCK_M, DSV4_ERR_UNSUPPORTED, "gemm: block_m %d unsupported (%d)", block_m,
-          DSV4_GEMM_BLOCK_M);
+  REQUIRE(moe_gemm_supported_block_m(block_m), DSV4_ERR_UNSUPPORTED,
+          "gemm: block_m %d unsupported (16, 64 or 128)", block_m);
   REQUIRE(D > 0 && D % 256 == 0, DSV4_ERR_UNSUPPORTED, "gemm down: D=%d not a multiple of 256", D);
   if (R == 0 || max_blocks == 0) return DSV4_OK;
   int rc = check_gemm_common(afmt, a, a_scale, sorted_ids, block_expert, num_post_padded, R, max_blocks,
@@ -226,12 +226,19 @@ int dsv4_moe_gemm_down(int afmt, const void* a, const void* a_scale, const int32
 struct LayerWs {
   int64_t sorted_ids, block_expert, npp, status, xa, xs, h, ha, hs, out, total;
   int max_blocks;
+  int bm;
 };
+
+// Rows per M block: 16 (decode kernel, ~1-4 rows per active expert) below 2048
+// routed rows, 64 (tiled kernel, weight tiles reused across 4 row subtiles)
+// from there on, where the Zipf-hot experts receive hundreds of rows.
+static int layer_block_m(int64_t R) { return R >= 2048 ? 64 : DSV4_GEMM_BLOCK_M; }
 
 static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile) {
   LayerWs w{};
   const int64_t R = (int64_t)T * K;
-  const int bm = DSV4_GEMM_BLOCK_M;
+  const int bm = layer_block_m(R);
+  w.bm = bm;
   w.max_blocks = dsv4_moe_align_max_blocks((int)R, E, bm);
   const bool fp8 = profile == DSV4_PROFILE_BF16;
   int64_t o = 0;
@@ -279,7 +286,7 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
   int32_t* npp = (int32_t*)(base + w.npp);
   int32_t* status = (int32_t*)(base + w.status);
   const int R = T * K;
-  const int bm = DSV4_GEMM_BLOCK_M;
+  const int bm = w.bm;
   int rc = dsv4_moe_align(topk_ids, ids_int64, nullptr, T, K, E, bm, w.max_blocks, sorted_ids, block_expert, npp,
                           nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, status,
                           stream);

@@ -138,6 +138,36 @@ DSV4_DEV void compute(v4f* acc, const AStage<AFMT>& a, const BStage& b) {
   }
 }
 
+// Epilogue of one 16-row subtile: lane holds rows row0 + 4*g + i (i = 0..3) of
+// column r16 of each of the 4 tiles.
+template <bool GATEUP>
+DSV4_DEV void store_tile(const Dsv4GemmArgs& p, const v4f* acc, int row0, int col0, int g, int r16) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int f = p.sorted_ids[row0 + 4 * g + i];
+    if (f >= p.R) continue;
+    uint16_t* orow = p.out + (int64_t)f * p.N + col0 + r16;
+    if (GATEUP) {
+      // deepseek_v4.py:177-187: bf16 GEMM outputs -> fp32, clamp, silu(gate) * up * w
+      const float w = p.topk_w[f];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float gt = dsv4::bf16_to_f32(dsv4::f32_to_bf16(acc[t][i]));
+        float up = dsv4::bf16_to_f32(dsv4::f32_to_bf16(acc[t + 2][i]));
+        if (p.swiglu_limit > 0.0f) {
+          up = fminf(fmaxf(up, -p.swiglu_limit), p.swiglu_limit);
+          gt = fminf(gt, p.swiglu_limit);
+        }
+        const float h = gt / (1.0f + expf(-gt)) * up * w;
+        orow[16 * t] = (uint16_t)dsv4::f32_to_bf16(h);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < kNT; ++t) orow[16 * t] = (uint16_t)dsv4::f32_to_bf16(acc[t][i]);
+    }
+  }
+}
+
 template <int AFMT, bool GATEUP, int NST>
 __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -211,51 +241,193 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
     }
   }
 
-  // Epilogue: lane holds rows 4*g + i (i = 0..3) of column r16 of each tile.
+  store_tile<GATEUP>(p, acc, mb * kBM, col0, g, r16);
+}
+
+// ---------------------------------------------------------------------------
+// Tiled variant for many rows per expert (prefill): one workgroup = 4 waves =
+// BM = 16*MT padded rows of one expert x 4 x 4 output tiles. The gathered A rows
+// of each 256-wide K stage are loaded once into a double-buffered LDS tile that
+// the four waves share; each wave streams its own four weight tiles from HBM
+// (one-stage register prefetch, as above) and reuses every weight fragment
+// across the MT row subtiles. One barrier per stage. The grid's x extent (N
+// tiles) is a multiple of 8, so all M blocks of one (expert, N tile) land on the
+// same XCD and re-read the weight tile from its L2.
+// ---------------------------------------------------------------------------
+template <int AFMT, int MT>
+DSV4_DEV void compute_tiled(v4f (*acc)[kNT], const uint8_t* lds, const uint32_t* sl, const BStage& b, int r16,
+                            int g) {
+  constexpr int ASB = AFMT == 0 ? 256 : 128;
+  constexpr int AROW = ASB + 16;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int f = p.sorted_ids[mb * kBM + 4 * g + i];
-    if (f >= p.R) continue;
-    uint16_t* orow = p.out + (int64_t)f * p.N + col0 + r16;
-    if (GATEUP) {
-      // deepseek_v4.py:177-187: bf16 GEMM outputs -> fp32, clamp, silu(gate) * up * w
-      const float w = p.topk_w[f];
+  for (int ji = 0; ji < 2; ++ji) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        float gt = dsv4::bf16_to_f32(dsv4::f32_to_bf16(acc[t][i]));
-        float up = dsv4::bf16_to_f32(dsv4::f32_to_bf16(acc[t + 2][i]));
-        if (p.swiglu_limit > 0.0f) {
-          up = fminf(fmaxf(up, -p.swiglu_limit), p.swiglu_limit);
-          gt = fminf(gt, p.swiglu_limit);
-        }
-        const float h = gt / (1.0f + expf(-gt)) * up * w;
-        orow[16 * t] = (uint16_t)dsv4::f32_to_bf16(h);
+    for (int mt = 0; mt < MT; ++mt) {
+      const int row = 16 * mt + r16;
+      const uint8_t* ap = lds + row * AROW;
+      v8i av;
+      if constexpr (AFMT == 1) {
+        const v4i lo = *(const v4i*)(ap + (2 * g + ji) * 16);
+        av = v8i{lo.x, lo.y, lo.z, lo.w, 0, 0, 0, 0};
+      } else {
+        const int o = 64 * (g >> 1) + 32 * ji + 16 * (g & 1);
+        const v4i lo = *(const v4i*)(ap + o);
+        const v4i hi = *(const v4i*)(ap + o + 128);
+        av = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       }
-    } else {
+      const int sa = (int)((sl[row * 2 + (g >> 1)] >> (8 * (2 * (g & 1) + ji))) & 0xffu);
 #pragma unroll
-      for (int t = 0; t < kNT; ++t) orow[16 * t] = (uint16_t)dsv4::f32_to_bf16(acc[t][i]);
+      for (int t = 0; t < kNT; ++t) {
+        const v8i bv = v8i{b.d[t][ji].x, b.d[t][ji].y, b.d[t][ji].z, b.d[t][ji].w, 0, 0, 0, 0};
+        const int sb = (int)((b.s[t] >> (8 * ji)) & 0xffu);
+        acc[mt][t] =
+            __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc[mt][t], AFMT == 0 ? 0 : 4, 4, 0, sa, 0, sb);
+      }
     }
   }
+}
+
+template <int AFMT, bool GATEUP, int NST, int MT>
+__global__ __launch_bounds__(256, (MT <= 4 ? 2 : 1)) void moe_gemm_tiled_kernel(Dsv4GemmArgs p) {
+  constexpr int BM = 16 * MT;
+  constexpr int ASB = AFMT == 0 ? 256 : 128;  // A bytes per row per stage
+  constexpr int AROW = ASB + 16;              // padded LDS row stride
+  constexpr int TPR = 256 / BM;               // loader threads per row
+  constexpr int LB = ASB / TPR;               // bytes one loader thread moves per stage
+  constexpr int LV = LB / 16;
+  static_assert(LV >= 1 && LB % 16 == 0, "loader granularity");
+  __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][BM * AROW];
+  __shared__ uint32_t s_lds[2][BM * 2];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int mb = blockIdx.y;
+  if (mb * BM >= p.num_post_padded[0]) return;
+  const int e = p.block_expert[mb];
+  const Dsv4ExpertPtrs ex = p.experts[e];
+  const bool have_w = GATEUP ? (ex.w1p && ex.w1s && ex.w3p && ex.w3s) : (ex.w2p && ex.w2s);
+  const int r16 = lane & 15, g = lane >> 4;
+
+  // loader role: thread -> (row lr, byte range lp*LB of the row's stage chunk)
+  const int lr = tid / TPR, lp = tid % TPR;
+  const int lf = p.sorted_ids[mb * BM + lr];
+  const int64_t larow = lf < p.R ? (int64_t)(lf / p.a_row_div) : 0;
+  const uint8_t* lsrc = p.a + larow * p.a_row_bytes + lp * LB;
+  const uint8_t* lssrc = p.a_scale + larow * (int64_t)(p.Kdim / 32);
+
+  const int64_t brow_bytes = p.Kdim / 2, bsrow = p.Kdim / 32;
+  int col0;
+  const uint8_t* bt[kNT];
+  const uint8_t* bst[kNT];
+  if (GATEUP) {
+    col0 = blockIdx.x * 128 + wave * 32;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int64_t row = col0 + 16 * t + r16;
+      bt[t] = ex.w1p + row * brow_bytes;
+      bst[t] = ex.w1s + row * bsrow;
+      bt[t + 2] = ex.w3p + row * brow_bytes;
+      bst[t + 2] = ex.w3s + row * bsrow;
+    }
+  } else {
+    col0 = blockIdx.x * 256 + wave * 64;
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) {
+      const int64_t row = col0 + 16 * t + r16;
+      bt[t] = ex.w2p + row * brow_bytes;
+      bst[t] = ex.w2s + row * bsrow;
+    }
+  }
+
+  v4f acc[MT][kNT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) acc[mt][t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  if (have_w) {  // uniform per workgroup, so the barriers below are reached by all
+    v4i lreg[LV];
+    uint32_t sreg0 = 0, sreg1 = 0;
+    BStage b[2];
+#pragma unroll
+    for (int v = 0; v < LV; ++v) lreg[v] = ld16(lsrc + 16 * v);
+    if (lp == 0) {
+      sreg0 = *(const __attribute__((address_space(1))) uint32_t*)(lssrc);
+      sreg1 = *(const __attribute__((address_space(1))) uint32_t*)(lssrc + 4);
+    }
+    load_b(b[0], bt, bst, 0, g);
+#pragma unroll
+    for (int v = 0; v < LV; ++v) *(v4i*)&a_lds[0][lr * AROW + lp * LB + 16 * v] = lreg[v];
+    if (lp == 0) {
+      s_lds[0][lr * 2] = sreg0;
+      s_lds[0][lr * 2 + 1] = sreg1;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NST; ++j) {
+      if (j + 1 < NST) {
+#pragma unroll
+        for (int v = 0; v < LV; ++v) lreg[v] = ld16(lsrc + (j + 1) * ASB + 16 * v);
+        if (lp == 0) {
+          sreg0 = *(const __attribute__((address_space(1))) uint32_t*)(lssrc + (j + 1) * 8);
+          sreg1 = *(const __attribute__((address_space(1))) uint32_t*)(lssrc + (j + 1) * 8 + 4);
+        }
+        load_b(b[(j + 1) & 1], bt, bst, j + 1, g);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      compute_tiled<AFMT, MT>(acc, a_lds[j & 1], s_lds[j & 1], b[j & 1], r16, g);
+      __builtin_amdgcn_sched_barrier(0);
+      if (j + 1 < NST) {
+#pragma unroll
+        for (int v = 0; v < LV; ++v) *(v4i*)&a_lds[(j + 1) & 1][lr * AROW + lp * LB + 16 * v] = lreg[v];
+        if (lp == 0) {
+          s_lds[(j + 1) & 1][lr * 2] = sreg0;
+          s_lds[(j + 1) & 1][lr * 2 + 1] = sreg1;
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) store_tile<GATEUP>(p, acc[mt], mb * BM + 16 * mt, col0, g, r16);
 }
 
 }  // namespace
 
 template <bool GATEUP, int NST>
-static void launch_nst(const Dsv4GemmArgs& a, dim3 grid, hipStream_t st) {
-  if (a.afmt == 0)
-    hipLaunchKernelGGL((moe_gemm_kernel<0, GATEUP, NST>), grid, dim3(64 * kWaves), 0, st, a);
-  else
-    hipLaunchKernelGGL((moe_gemm_kernel<1, GATEUP, NST>), grid, dim3(64 * kWaves), 0, st, a);
+static void launch_nst(const Dsv4GemmArgs& a, hipStream_t st) {
+  const int cols_per_wave = GATEUP ? 32 : 64;
+  if (a.block_m == kBM) {  // decode-shaped: single-wave workgroups
+    const dim3 grid(a.N / (kWaves * cols_per_wave), a.max_blocks);
+    if (a.afmt == 0)
+      hipLaunchKernelGGL((moe_gemm_kernel<0, GATEUP, NST>), grid, dim3(64 * kWaves), 0, st, a);
+    else
+      hipLaunchKernelGGL((moe_gemm_kernel<1, GATEUP, NST>), grid, dim3(64 * kWaves), 0, st, a);
+    return;
+  }
+  const dim3 grid(a.N / (4 * cols_per_wave), a.max_blocks);
+  if (a.block_m == 64) {
+    if (a.afmt == 0)
+      hipLaunchKernelGGL((moe_gemm_tiled_kernel<0, GATEUP, NST, 4>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((moe_gemm_tiled_kernel<1, GATEUP, NST, 4>), grid, dim3(256), 0, st, a);
+  } else {
+    if (a.afmt == 0)
+      hipLaunchKernelGGL((moe_gemm_tiled_kernel<0, GATEUP, NST, 8>), grid, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((moe_gemm_tiled_kernel<1, GATEUP, NST, 8>), grid, dim3(256), 0, st, a);
+  }
 }
 
 template <bool GATEUP>
-static hipError_t launch(const Dsv4GemmArgs& a, dim3 grid, hipStream_t st) {
+static hipError_t launch(const Dsv4GemmArgs& a, hipStream_t st) {
+  if (a.block_m != 16 && a.block_m != 64 && a.block_m != 128) return hipErrorInvalidValue;
   switch (a.Kdim / kStageK) {
-    case 2: launch_nst<GATEUP, 2>(a, grid, st); break;
-    case 4: launch_nst<GATEUP, 4>(a, grid, st); break;
-    case 8: launch_nst<GATEUP, 8>(a, grid, st); break;
-    case 16: launch_nst<GATEUP, 16>(a, grid, st); break;
-    case 32: launch_nst<GATEUP, 32>(a, grid, st); break;
+    case 2: launch_nst<GATEUP, 2>(a, st); break;
+    case 4: launch_nst<GATEUP, 4>(a, st); break;
+    case 8: launch_nst<GATEUP, 8>(a, st); break;
+    case 16: launch_nst<GATEUP, 16>(a, st); break;
+    case 32: launch_nst<GATEUP, 32>(a, st); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -266,10 +438,8 @@ bool moe_gemm_supported_kdim(int kdim) {
   return kdim % kStageK == 0 && (n == 2 || n == 4 || n == 8 || n == 16 || n == 32);
 }
 
-hipError_t launch_moe_gemm_gateup(const Dsv4GemmArgs& a, hipStream_t st) {
-  return launch<true>(a, dim3(a.N / (kWaves * 32), a.max_blocks), st);
-}
+bool moe_gemm_supported_block_m(int bm) { return bm == 16 || bm == 64 || bm == 128; }
 
-hipError_t launch_moe_gemm_down(const Dsv4GemmArgs& a, hipStream_t st) {
-  return launch<false>(a, dim3(a.N / (kWaves * 64), a.max_blocks), st);
-}
+hipError_t launch_moe_gemm_gateup(const Dsv4GemmArgs& a, hipStream_t st) { return launch<true>(a, st); }
+
+hipError_t launch_moe_gemm_down(const Dsv4GemmArgs& a, hipStream_t st) { return launch<false>(a, st); }

@@ -55,10 +55,13 @@ def _case(T, K, E, D, I, seed, dev):
 
 
 @pytest.mark.parametrize("profile", ["bf16", "a4w4"])
-@pytest.mark.parametrize("T,K,E,D,I", [(24, 4, 16, 1024, 512), (200, 8, 16, 512, 512), (8, 8, 256, 4096, 2048)])
-def test_grouped_gemm_stages(gpu, profile, T, K, E, D, I):
+@pytest.mark.parametrize("T,K,E,D,I,bm", [(24, 4, 16, 1024, 512, 16), (200, 8, 16, 512, 512, 16),
+                                          (8, 8, 256, 4096, 2048, 16), (200, 8, 16, 512, 512, 64),
+                                          (200, 8, 16, 1024, 512, 128), (300, 6, 24, 2048, 1024, 64)])
+def test_grouped_gemm_stages(gpu, profile, T, K, E, D, I, bm):
+    # bm 16 runs the single-wave decode kernel, 64/128 the LDS-tiled kernel
     ids, w, xb, host, devw, table = _case(T, K, E, D, I, 31 + T, gpu)
-    al = ops.moe_align(_dev(ids, gpu), _dev(w, gpu), E, 16)
+    al = ops.moe_align(_dev(ids, gpu), _dev(w, gpu), E, bm)
     R = T * K
     if profile == "bf16":
         rt, codes, s, k = Q.act_quant(xb, 128)
@@ -128,8 +131,9 @@ def test_grouped_gemm_empty_group_pattern(gpu):
 
 
 @pytest.mark.parametrize("profile", ["bf16", "a4w4"])
-@pytest.mark.parametrize("T,K,E,D,I", [(8, 8, 256, 4096, 2048), (64, 6, 32, 1024, 512)])
+@pytest.mark.parametrize("T,K,E,D,I", [(8, 8, 256, 4096, 2048), (64, 6, 32, 1024, 512), (256, 8, 32, 2048, 1024)])
 def test_layer_forward_vs_oracle(gpu, profile, T, K, E, D, I):
+    # 256 tokens x top-8 = 2048 routed rows: the layer switches to 64-row M blocks (tiled kernel)
     ids, w, xb, host, devw, table = _case(T, K, E, D, I, 77 + T, gpu)
     runner = ops.LayerRunner(gpu, E, D, I)
     x = _dev_bf16(xb, gpu)
