@@ -12,8 +12,10 @@ Prints ONE JSON line. ``value`` = decode tokens/s through the layer.
 ``roofline`` = the dominant kernel (gate/up GEMM) - algorithmic bytes per
 launch over its HIP-event-timed average duration, against 8 TB/s HBM.
 ``cpu_baseline`` = the numpy oracle of the same layer on one host core.
-``extra`` = dequant GB/s (config-0 matrices), a4w4 decode (64 tokens) and
-prefill (2048 tokens) in both profiles.
+``extra`` = dequant GB/s (config-0 matrices), a4w4 decode (64 tokens),
+prefill (2048 tokens) in both profiles, and expert offload (8 layers x 256
+experts in pinned host memory, 512 device slots, 512 drifting-Zipf decode
+steps: hit rate, H2D traffic and layer tokens/s with exposed copy time).
 """
 
 import argparse
@@ -46,7 +48,9 @@ def parse():
     ap.add_argument("--layers", type=int, default=8, help="distinct expert-weight sets cycled through")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
-    ap.add_argument("--only", default="", help="profile helper: run only 'decode', 'dequant' or 'prefill'")
+    ap.add_argument("--only", default="",
+                    help="profile helper: run only 'decode', 'dequant', 'prefill' or 'offload'")
+    ap.add_argument("--offload-steps", type=int, default=512, help="decode steps of the expert-offload leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy 1 GiB device-to-device (a plain copy of known size for counter calibration)")
     return ap.parse_args()
@@ -171,8 +175,100 @@ def measure_dequant(dev, gen, n_mats=64, reps=5):
     e1.synchronize()
     t = e0.elapsed_time(e1) * 1e-3 / (reps * n_mats)
     per = N * K * 2.53125
-    return {"gbs": per / t / 1e9, "frac_hbm": per / t / 1e9 / HBM_PEAK_GBS, "us_per_matrix": t * 1e6,
+    # the same 64 matrices as one [64*2048, 4096] launch: kernel throughput without the
+    # per-call host overhead of the Python wrapper
+    big_p, big_s, big_o = packed.view(n_mats * N, K // 2), scales.view(n_mats * N, K // 32), out.view(n_mats * N, K)
+    e0.record()
+    for _ in range(reps):
+        ops.dequant_mxfp4(big_p, big_s, out=big_o)
+    e1.record()
+    e1.synchronize()
+    tb = e0.elapsed_time(e1) * 1e-3 / reps
+    gbs_b = per * n_mats / tb / 1e9
+    return {"gbs": gbs_b, "frac_hbm": gbs_b / HBM_PEAK_GBS, "batched_us": tb * 1e6,
+            "per_matrix_call_gbs": per / t / 1e9, "us_per_matrix_call": t * 1e6,
             "bytes_per_matrix": per, "matrices": n_mats}
+
+
+def measure_pcie(dev, record_bytes):
+    """Pinned host -> device copy rate: one expert record at a time (16 back to back) and 1 GiB."""
+    out = {}
+    for name, nbytes, reps in (("record", record_bytes, 16), ("1GiB", 1 << 30, 3)):
+        src = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+        src.fill_(1)
+        dst = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        dst.copy_(src, non_blocking=True)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            dst.copy_(src, non_blocking=True)
+        e1.record()
+        e1.synchronize()
+        out[f"h2d_{name}_gbs"] = nbytes * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+        del src, dst
+    return out
+
+
+def measure_offload(dev, n_steps=512, n_layers=8, n_slots=512, T=8, K=8, warmup_steps=32):
+    """Expert offload: every layer's 256 experts in a pinned host pool, ``n_slots`` device
+    slots shared by all layers (LRU), decode steps of T tokens with per-layer Zipf routing
+    whose hot set drifts. A miss is one record copy on the slot cache's copy stream; the
+    compute stream waits for it, so exposed copy time is part of the layer time. Host-side
+    work (unique ids, slot acquisition, table upload) is inside the timed region, as it is
+    for a serving loop."""
+    from dsv4_hip import ops, synth, PROFILE_BF16, RULE_OCP_FLOOR
+    from dsv4_hip.slots import SlotCache, SlotLayout
+    base = [{k: torch.from_numpy(v) for k, v in synth.expert_weights(e, D, I).items()} for e in range(8)]
+    layout = SlotLayout(base[0])
+    t0 = time.perf_counter()
+    cache = SlotCache(dev, n_slots, layout, pin=True)
+    pinned = True
+    for l in range(n_layers):
+        for e in range(E):
+            pinned &= cache.register(l, e, base[(l * 7 + e) % len(base)])
+    t_reg = time.perf_counter() - t0
+    route = synth.DriftingZipf(n_layers, E, K)
+    total = warmup_steps + n_steps
+    ids_all = np.stack([np.stack(route.step(T)) for _ in range(total)])       # [steps, L, T, K]
+    w_all = np.stack([synth.routing_weights(T, K, 1000 + s) for s in range(total)])
+    ids_dev = torch.from_numpy(ids_all).to(dev)
+    w_dev = torch.from_numpy(w_all).to(dev)
+    uniq = [[np.unique(ids_all[s, l]).astype(np.int32) for l in range(n_layers)] for s in range(total)]
+    x = synth.bf16_normal(np.random.default_rng(6), (T, D)).to(dev)
+    runner = ops.LayerRunner(dev, E, D, I)
+    ys = [torch.empty((T, D), dtype=torch.bfloat16, device=dev) for _ in range(n_layers)]
+
+    def run(s0, s1):
+        for s in range(s0, s1):
+            for l in range(n_layers):
+                slots, _ = cache.acquire(l, uniq[s][l])
+                table = cache.table(uniq[s][l], slots, E)
+                runner.forward(x, ids_dev[s, l], w_dev[s], table, profile=PROFILE_BF16, rule=RULE_OCP_FLOOR,
+                               out=ys[l])
+
+    run(0, warmup_steps)
+    torch.cuda.synchronize()
+    cache.reset_stats()
+    t0 = time.perf_counter()
+    run(warmup_steps, total)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    st = cache.stats()
+    layer_s = wall / (n_steps * n_layers)
+    lookups = st["hits"] + st["misses"]
+    res = {"layers": n_layers, "experts_per_layer": E, "slots": n_slots, "steps": n_steps, "tokens_per_step": T,
+           "host_pool_gb": n_layers * E * layout.record_bytes / 1e9, "host_pool_pinned": bool(pinned),
+           "slot_pool_gb": n_slots * layout.record_bytes / 1e9, "register_s": t_reg,
+           "ms_per_layer": layer_s * 1e3, "layer_tokens_per_s": T / layer_s, "step_tokens_per_s": T / (wall / n_steps),
+           "hit_rate": st["hits"] / max(lookups, 1), "misses_per_step": st["misses"] / n_steps,
+           "h2d_gb": st["bytes_h2d"] / 1e9, "h2d_effective_gbs": st["bytes_h2d"] / wall / 1e9,
+           "evictions": st["evictions"]}
+    res.update(measure_pcie(dev, layout.record_bytes))
+    cache.close()
+    del cache, ys, runner
+    torch.cuda.empty_cache()
+    return res
 
 
 def cpu_baseline(sample_steps=1):
@@ -274,6 +370,8 @@ def main():
                            "frac_hbm": byts / s2 / 1e9 / HBM_PEAK_GBS, "active_experts": A}
         del pools, tables
         torch.cuda.empty_cache()
+    if not args.no_extra and args.only in ("", "offload") and args.offload_steps > 0:
+        extra["offload_config4"] = measure_offload(dev, n_steps=args.offload_steps)
     if extra:
         line["extra"] = extra
     if not args.no_cpu_baseline and args.only == "":

@@ -51,64 +51,33 @@ DSV4_DEV u32x4 dequant8(uint32_t p, uint32_t s) {
   return r;
 }
 
-#ifndef DSV4_DEQUANT_BLOCK_PER_LANE
-#define DSV4_DEQUANT_BLOCK_PER_LANE 0
-#endif
-
-// One lane per 32-element scale block: a 16-byte load of packed nibbles plus
-// one scale byte in, four 16-byte stores out. Consecutive lanes own
-// consecutive blocks, so a wave reads 1 KB and writes 4 KB of contiguous memory
-// per block of work; two blocks per lane are kept in flight.
-__global__ __launch_bounds__(256) void mxfp4_dequant_block_kernel(const u32x4* __restrict__ packed,
-                                                                   const uint8_t* __restrict__ scales,
-                                                                   u32x4* __restrict__ out, int64_t n_blocks) {
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  for (; b + stride < n_blocks; b += 2 * stride) {
-    const u32x4 p0 = __builtin_nontemporal_load(packed + b);
-    const u32x4 p1 = __builtin_nontemporal_load(packed + b + stride);
-    const uint32_t s0 = scales[b], s1 = scales[b + stride];
-    u32x4* o0 = out + 4 * b;
-    u32x4* o1 = out + 4 * (b + stride);
-    __builtin_nontemporal_store(dequant8(p0.x, s0), o0);
-    __builtin_nontemporal_store(dequant8(p0.y, s0), o0 + 1);
-    __builtin_nontemporal_store(dequant8(p0.z, s0), o0 + 2);
-    __builtin_nontemporal_store(dequant8(p0.w, s0), o0 + 3);
-    __builtin_nontemporal_store(dequant8(p1.x, s1), o1);
-    __builtin_nontemporal_store(dequant8(p1.y, s1), o1 + 1);
-    __builtin_nontemporal_store(dequant8(p1.z, s1), o1 + 2);
-    __builtin_nontemporal_store(dequant8(p1.w, s1), o1 + 3);
-  }
-  for (; b < n_blocks; b += stride) {
-    const u32x4 p = packed[b];
-    const uint32_t s = scales[b];
-    out[4 * b] = dequant8(p.x, s);
-    out[4 * b + 1] = dequant8(p.y, s);
-    out[4 * b + 2] = dequant8(p.z, s);
-    out[4 * b + 3] = dequant8(p.w, s);
-  }
-}
+// Four 8-element groups per thread, spaced one grid-stride apart, so each
+// load/store instruction of a wave still covers one contiguous span while four
+// independent loads are in flight per lane. Output is written with
+// non-temporal stores (it is not re-read by this kernel). The launcher sizes
+// the grid so that 4 * grid * 256 >= n_groups; the guards only bite in the
+// last workgroups.
+constexpr int kDequantGroupsPerThread = 4;
 
 __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint32_t* __restrict__ packed,
                                                              const uint8_t* __restrict__ scales,
                                                              u32x4* __restrict__ out, int64_t n_groups) {
   const int64_t stride = (int64_t)gridDim.x * 256;
-  int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  // four independent groups in flight per thread
-  for (; g + 3 * stride < n_groups; g += 4 * stride) {
-    uint32_t p0 = __builtin_nontemporal_load(packed + g);
-    uint32_t p1 = __builtin_nontemporal_load(packed + g + stride);
-    uint32_t p2 = __builtin_nontemporal_load(packed + g + 2 * stride);
-    uint32_t p3 = __builtin_nontemporal_load(packed + g + 3 * stride);
-    uint32_t s0 = scales[g >> 2], s1 = scales[(g + stride) >> 2];
-    uint32_t s2 = scales[(g + 2 * stride) >> 2], s3 = scales[(g + 3 * stride) >> 2];
-    u32x4 r0 = dequant8(p0, s0), r1 = dequant8(p1, s1), r2 = dequant8(p2, s2), r3 = dequant8(p3, s3);
-    __builtin_nontemporal_store(r0, out + g);
-    __builtin_nontemporal_store(r1, out + g + stride);
-    __builtin_nontemporal_store(r2, out + g + 2 * stride);
-    __builtin_nontemporal_store(r3, out + g + 3 * stride);
+  const int64_t g0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  uint32_t p[kDequantGroupsPerThread], s[kDequantGroupsPerThread];
+#pragma unroll
+  for (int i = 0; i < kDequantGroupsPerThread; ++i) {
+    const int64_t g = g0 + i * stride;
+    if (g < n_groups) {
+      p[i] = __builtin_nontemporal_load(packed + g);
+      s[i] = scales[g >> 2];
+    }
   }
-  for (; g < n_groups; g += stride) out[g] = dequant8(packed[g], scales[g >> 2]);
+#pragma unroll
+  for (int i = 0; i < kDequantGroupsPerThread; ++i) {
+    const int64_t g = g0 + i * stride;
+    if (g < n_groups) __builtin_nontemporal_store(dequant8(p[i], s[i]), out + g);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -229,20 +198,12 @@ __global__ __launch_bounds__(256) void mxfp4_act_quant_kernel(const uint4* __res
 // ---------------------------------------------------------------------------
 hipError_t launch_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, uint16_t* out,
                                 int64_t n_elems, hipStream_t st) {
-  if (DSV4_DEQUANT_BLOCK_PER_LANE && ((uintptr_t)packed & 15) == 0) {
-    const int64_t n_blocks = n_elems / 32;
-    if (n_blocks == 0) return hipSuccess;
-    const int64_t want = (n_blocks + 511) / 512;  // two blocks per lane
-    const int grid = (int)(want < 16384 ? want : 16384);
-    hipLaunchKernelGGL(mxfp4_dequant_block_kernel, dim3(grid), dim3(256), 0, st, (const u32x4*)packed, scales,
-                       (u32x4*)out, n_blocks);
-    return hipGetLastError();
-  }
-  int64_t n_groups = n_elems / 8;
+  const int64_t n_groups = n_elems / 8;
   if (n_groups == 0) return hipSuccess;
-  int64_t want = (n_groups + 255) / 256;
-  int grid = (int)(want < 8192 ? want : 8192);
-  hipLaunchKernelGGL(mxfp4_dequant_kernel, dim3(grid), dim3(256), 0, st,
+  const int64_t per_wg = 256LL * kDequantGroupsPerThread;
+  const int64_t grid = (n_groups + per_wg - 1) / per_wg;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(mxfp4_dequant_kernel, dim3((unsigned)grid), dim3(256), 0, st,
                      (const uint32_t*)packed, scales, (u32x4*)out, n_groups);
   return hipGetLastError();
 }
