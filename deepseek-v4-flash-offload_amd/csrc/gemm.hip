@@ -90,7 +90,66 @@ DSV4_DEV v4i ld16_stream(const uint8_t* p) { return *(gv4i*)p; }
 #endif
 DSV4_DEV uint32_t ld_u16(const uint8_t* p) { return *(gu16*)p; }
 
-template <int AFMT>
+// ---------------------------------------------------------------------------
+// Scale bytes, loaded once per row instead of once per stage. Per stage a lane
+// needs 2 scale bytes of each of its rows (bytes 8j + 2g, +1: one per MFMA of
+// the stage); fetching them stage by stage issues one L1->L2 request per row
+// per stage for 2 bytes, and those requests, not the bytes, were measured to
+// bound the weight stream (the per-CU pool of outstanding L1 misses fills with
+// them). Instead the four lane groups of a row load the row's K/32 scale bytes
+// once, each group a contiguous S = K/128 byte slice, and every stage fetches
+// its two bytes from the holding lane with a cross-lane permute.
+// ---------------------------------------------------------------------------
+template <int NST>
+struct RowScales {
+  static constexpr int S = 2 * NST;  // bytes per lane group
+  uint32_t w[S / 4 > 0 ? S / 4 : 1];
+};
+
+template <int NST>
+DSV4_DEV void load_row_scales(RowScales<NST>& rs, const uint8_t* row, int g) {
+  constexpr int S = RowScales<NST>::S;
+  const uint8_t* p = row + g * S;
+  if constexpr (S >= 16) {
+#pragma unroll
+    for (int i = 0; i < S / 16; ++i) {
+      const v4i v = ld16(p + 16 * i);
+      rs.w[4 * i] = (uint32_t)v.x;
+      rs.w[4 * i + 1] = (uint32_t)v.y;
+      rs.w[4 * i + 2] = (uint32_t)v.z;
+      rs.w[4 * i + 3] = (uint32_t)v.w;
+    }
+  } else if constexpr (S == 8) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    typedef __attribute__((address_space(1))) const u32x2 gu32x2;
+    const u32x2 v = *(gu32x2*)p;
+    rs.w[0] = v.x;
+    rs.w[1] = v.y;
+  } else {
+    typedef __attribute__((address_space(1))) const uint32_t gu32;
+    rs.w[0] = *(gu32*)p;
+  }
+}
+
+// The 2 scale bytes (low byte: MFMA ji = 0) lane (r16, g) uses in stage j.
+template <int NST>
+DSV4_DEV uint32_t stage_scales(const RowScales<NST>& rs, int j, int r16, int g) {
+  constexpr int S = RowScales<NST>::S;
+  if constexpr (S >= 8) {
+    // bytes [8j, 8j+8) sit in one lane group: dwords d0, d0 + 1
+    const int holder = (8 * j) / S, d0 = ((8 * j) % S) / 4;
+    const int src = r16 + 16 * holder;
+    const uint32_t v0 = (uint32_t)__shfl((int)rs.w[d0], src, 64);
+    const uint32_t v1 = (uint32_t)__shfl((int)rs.w[d0 + 1], src, 64);
+    return (((g & 2) ? v1 : v0) >> (16 * (g & 1))) & 0xffffu;
+  } else {  // S == 4 (K = 512): a stage spans two lane groups
+    const int src = r16 + 16 * (2 * j + (g >> 1));
+    const uint32_t v = (uint32_t)__shfl((int)rs.w[0], src, 64);
+    return (v >> (16 * (g & 1))) & 0xffffu;
+  }
+}
+
+template <int AFMT, bool SCALES = true>
 DSV4_DEV void load_a(AStage<AFMT>& a, const uint8_t* abase, const uint8_t* asbase, int j, int g) {
   if constexpr (AFMT == 1) {
     const uint8_t* p = abase + (int64_t)j * 128 + g * 32;
@@ -105,16 +164,17 @@ DSV4_DEV void load_a(AStage<AFMT>& a, const uint8_t* abase, const uint8_t* asbas
       a.d[ji] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
     }
   }
-  a.s = ld_u16(asbase + j * 8 + 2 * g);
+  if constexpr (SCALES) a.s = ld_u16(asbase + j * 8 + 2 * g);
 }
 
+template <bool SCALES = true>
 DSV4_DEV void load_b(BStage& b, const uint8_t* const* bt, const uint8_t* const* bst, int j, int g) {
 #pragma unroll
   for (int t = 0; t < kNT; ++t) {
     const uint8_t* p = bt[t] + (int64_t)j * 128 + g * 32;
     b.d[t][0] = ld16_stream(p);
     b.d[t][1] = ld16_stream(p + 16);
-    b.s[t] = ld_u16(bst[t] + j * 8 + 2 * g);
+    if constexpr (SCALES) b.s[t] = ld_u16(bst[t] + j * 8 + 2 * g);
   }
 }
 
@@ -224,18 +284,25 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
     constexpr int RING = P + 1;
     AStage<AFMT> a[RING];
     BStage b[RING];
+    RowScales<NST> as_row, bs_row[kNT];
+    load_row_scales<NST>(as_row, asbase, g);
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) load_row_scales<NST>(bs_row[t], bst[t], g);
 #pragma unroll
     for (int j = 0; j < P && j < NST; ++j) {
-      load_a<AFMT>(a[j % RING], abase, asbase, j, g);
-      load_b(b[j % RING], bt, bst, j, g);
+      load_a<AFMT, false>(a[j % RING], abase, asbase, j, g);
+      load_b<false>(b[j % RING], bt, bst, j, g);
     }
 #pragma unroll
     for (int j = 0; j < NST; ++j) {
       if (j + P < NST) {
-        load_a<AFMT>(a[(j + P) % RING], abase, asbase, j + P, g);
-        load_b(b[(j + P) % RING], bt, bst, j + P, g);
+        load_a<AFMT, false>(a[(j + P) % RING], abase, asbase, j + P, g);
+        load_b<false>(b[(j + P) % RING], bt, bst, j + P, g);
       }
       if constexpr (P > 0) __builtin_amdgcn_sched_barrier(0);
+      a[j % RING].s = stage_scales<NST>(as_row, j, r16, g);
+#pragma unroll
+      for (int t = 0; t < kNT; ++t) b[j % RING].s[t] = stage_scales<NST>(bs_row[t], j, r16, g);
       compute<AFMT>(acc, a[j % RING], b[j % RING]);
       if constexpr (P > 0) __builtin_amdgcn_sched_barrier(0);
     }
@@ -255,8 +322,8 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
 // same XCD and re-read the weight tile from its L2.
 // ---------------------------------------------------------------------------
 template <int AFMT, int MT>
-DSV4_DEV void compute_tiled(v4f (*acc)[kNT], const uint8_t* lds, const uint32_t* sl, const BStage& b, int r16,
-                            int g) {
+DSV4_DEV void compute_tiled(v4f (*acc)[kNT], const uint8_t* lds, const uint8_t* as_tab, int as_pitch, int j,
+                            const BStage& b, int r16, int g) {
   constexpr int ASB = AFMT == 0 ? 256 : 128;
   constexpr int AROW = ASB + 16;
 #pragma unroll
@@ -275,7 +342,7 @@ DSV4_DEV void compute_tiled(v4f (*acc)[kNT], const uint8_t* lds, const uint32_t*
         const v4i hi = *(const v4i*)(ap + o + 128);
         av = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       }
-      const int sa = (int)((sl[row * 2 + (g >> 1)] >> (8 * (2 * (g & 1) + ji))) & 0xffu);
+      const int sa = as_tab[row * as_pitch + 8 * j + 2 * g + ji];
 #pragma unroll
       for (int t = 0; t < kNT; ++t) {
         const v8i bv = v8i{b.d[t][ji].x, b.d[t][ji].y, b.d[t][ji].z, b.d[t][ji].w, 0, 0, 0, 0};
@@ -292,12 +359,13 @@ __global__ __launch_bounds__(256, (MT <= 4 ? 2 : 1)) void moe_gemm_tiled_kernel(
   constexpr int BM = 16 * MT;
   constexpr int ASB = AFMT == 0 ? 256 : 128;  // A bytes per row per stage
   constexpr int AROW = ASB + 16;              // padded LDS row stride
-  constexpr int TPR = 256 / BM;               // loader threads per row
-  constexpr int LB = ASB / TPR;               // bytes one loader thread moves per stage
-  constexpr int LV = LB / 16;
-  static_assert(LV >= 1 && LB % 16 == 0, "loader granularity");
+  constexpr int LV = BM * ASB / (256 * 16);   // 16-byte A chunks one thread moves per stage
+  constexpr int KSB = 8 * NST;                // scale bytes per row (K / 32)
+  constexpr int ASP = KSB + 16;               // A scale table pitch: 16 rows on distinct banks
+  constexpr int AS_CHUNKS = BM * KSB / 16;
+  static_assert(LV >= 1 && LV * 256 * 16 == BM * ASB, "loader granularity");
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][BM * AROW];
-  __shared__ uint32_t s_lds[2][BM * 2];
+  __shared__ __attribute__((aligned(16))) uint8_t as_tab[BM * ASP];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int mb = blockIdx.y;
@@ -307,12 +375,20 @@ __global__ __launch_bounds__(256, (MT <= 4 ? 2 : 1)) void moe_gemm_tiled_kernel(
   const bool have_w = GATEUP ? (ex.w1p && ex.w1s && ex.w3p && ex.w3s) : (ex.w2p && ex.w2s);
   const int r16 = lane & 15, g = lane >> 4;
 
-  // loader role: thread -> (row lr, byte range lp*LB of the row's stage chunk)
-  const int lr = tid / TPR, lp = tid % TPR;
-  const int lf = p.sorted_ids[mb * BM + lr];
-  const int64_t larow = lf < p.R ? (int64_t)(lf / p.a_row_div) : 0;
-  const uint8_t* lsrc = p.a + larow * p.a_row_bytes + lp * LB;
-  const uint8_t* lssrc = p.a_scale + larow * (int64_t)(p.Kdim / 32);
+  // loader role: load v of wave w moves 1 KB of the stage's A tile = whole
+  // 128-byte lines (4 rows x 256 B for E4M3, 8 rows x 128 B for E2M1), so each
+  // line is one L1->L2 request; lane L carries 16-byte chunk (v*4 + w)*64 + L
+  constexpr int CPRW = ASB / 16;  // 16-byte chunks per A row per stage
+  const uint8_t* lsrc[LV];
+  int ldst[LV];
+#pragma unroll
+  for (int v = 0; v < LV; ++v) {
+    const int id = (v * 4 + wave) * 64 + lane, row = id / CPRW, ch = id % CPRW;
+    const int f = p.sorted_ids[mb * BM + row];
+    const int64_t ar = f < p.R ? (int64_t)(f / p.a_row_div) : 0;  // padding rows read row 0
+    lsrc[v] = p.a + ar * p.a_row_bytes + 16 * ch;
+    ldst[v] = row * AROW + 16 * ch;
+  }
 
   const int64_t brow_bytes = p.Kdim / 2, bsrow = p.Kdim / 32;
   int col0;
@@ -345,44 +421,44 @@ __global__ __launch_bounds__(256, (MT <= 4 ? 2 : 1)) void moe_gemm_tiled_kernel(
     for (int t = 0; t < kNT; ++t) acc[mt][t] = v4f{0.f, 0.f, 0.f, 0.f};
 
   if (have_w) {  // uniform per workgroup, so the barriers below are reached by all
+    // scales of the whole K range, loaded once: the weight rows' by their lanes
+    // (shared out per stage by permutes), the A rows' into an LDS table
+    RowScales<NST> bs_row[kNT];
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) load_row_scales<NST>(bs_row[t], bst[t], g);
+#pragma unroll
+    for (int i = 0; i < (AS_CHUNKS + 255) / 256; ++i) {
+      const int c = i * 256 + tid;
+      if (c < AS_CHUNKS) {
+        const int row = c / (KSB / 16), ch = c % (KSB / 16);
+        const int f = p.sorted_ids[mb * BM + row];
+        const int64_t ar = f < p.R ? (int64_t)(f / p.a_row_div) : 0;
+        *(v4i*)&as_tab[row * ASP + 16 * ch] = ld16(p.a_scale + ar * KSB + 16 * ch);
+      }
+    }
     v4i lreg[LV];
-    uint32_t sreg0 = 0, sreg1 = 0;
     BStage b[2];
 #pragma unroll
-    for (int v = 0; v < LV; ++v) lreg[v] = ld16(lsrc + 16 * v);
-    if (lp == 0) {
-      sreg0 = *(const __attribute__((address_space(1))) uint32_t*)(lssrc);
-      sreg1 = *(const __attribute__((address_space(1))) uint32_t*)(lssrc + 4);
-    }
-    load_b(b[0], bt, bst, 0, g);
+    for (int v = 0; v < LV; ++v) lreg[v] = ld16(lsrc[v]);
+    load_b<false>(b[0], bt, bst, 0, g);
 #pragma unroll
-    for (int v = 0; v < LV; ++v) *(v4i*)&a_lds[0][lr * AROW + lp * LB + 16 * v] = lreg[v];
-    if (lp == 0) {
-      s_lds[0][lr * 2] = sreg0;
-      s_lds[0][lr * 2 + 1] = sreg1;
-    }
+    for (int v = 0; v < LV; ++v) *(v4i*)&a_lds[0][ldst[v]] = lreg[v];
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < NST; ++j) {
       if (j + 1 < NST) {
 #pragma unroll
-        for (int v = 0; v < LV; ++v) lreg[v] = ld16(lsrc + (j + 1) * ASB + 16 * v);
-        if (lp == 0) {
-          sreg0 = *(const __attribute__((address_space(1))) uint32_t*)(lssrc + (j + 1) * 8);
-          sreg1 = *(const __attribute__((address_space(1))) uint32_t*)(lssrc + (j + 1) * 8 + 4);
-        }
-        load_b(b[(j + 1) & 1], bt, bst, j + 1, g);
+        for (int v = 0; v < LV; ++v) lreg[v] = ld16(lsrc[v] + (j + 1) * ASB);
+        load_b<false>(b[(j + 1) & 1], bt, bst, j + 1, g);
       }
       __builtin_amdgcn_sched_barrier(0);
-      compute_tiled<AFMT, MT>(acc, a_lds[j & 1], s_lds[j & 1], b[j & 1], r16, g);
+#pragma unroll
+      for (int t = 0; t < kNT; ++t) b[j & 1].s[t] = stage_scales<NST>(bs_row[t], j, r16, g);
+      compute_tiled<AFMT, MT>(acc, a_lds[j & 1], as_tab, ASP, j, b[j & 1], r16, g);
       __builtin_amdgcn_sched_barrier(0);
       if (j + 1 < NST) {
 #pragma unroll
-        for (int v = 0; v < LV; ++v) *(v4i*)&a_lds[(j + 1) & 1][lr * AROW + lp * LB + 16 * v] = lreg[v];
-        if (lp == 0) {
-          s_lds[(j + 1) & 1][lr * 2] = sreg0;
-          s_lds[(j + 1) & 1][lr * 2 + 1] = sreg1;
-        }
+        for (int v = 0; v < LV; ++v) *(v4i*)&a_lds[(j + 1) & 1][ldst[v]] = lreg[v];
       }
       __syncthreads();
     }
