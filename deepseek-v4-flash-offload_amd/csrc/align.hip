@@ -16,6 +16,7 @@
 //      carries across chunks.
 #include "common.h"
 #include "kernels.h"
+#include "quant_dev.h"
 
 namespace {
 
@@ -48,10 +49,8 @@ __device__ int block_exclusive_scan(int v, int* lds_waves, int* out_total) {
 }
 
 template <typename IdT, int NT>
-__global__ __launch_bounds__(NT) void moe_align_kernel(const IdT* __restrict__ ids,
-                                                       const float* __restrict__ topk_w, int R, int K,
-                                                       int E, int block_m, int max_blocks,
-                                                       Dsv4AlignOut o) {
+__device__ void align_body(const IdT* __restrict__ ids, const float* __restrict__ topk_w, int R, int K, int E,
+                           int block_m, int max_blocks, const Dsv4AlignOut& o) {
   constexpr int kThreads = NT;
   constexpr int kWaves = NT / 64;
   extern __shared__ int lds[];
@@ -150,6 +149,36 @@ __global__ __launch_bounds__(NT) void moe_align_kernel(const IdT* __restrict__ i
   }
 }
 
+template <typename IdT, int NT>
+__global__ __launch_bounds__(NT) void moe_align_kernel(const IdT* __restrict__ ids,
+                                                       const float* __restrict__ topk_w, int R, int K,
+                                                       int E, int block_m, int max_blocks,
+                                                       Dsv4AlignOut o) {
+  align_body<IdT, NT>(ids, topk_w, R, K, E, block_m, max_blocks, o);
+}
+
+// The layer's first launch: workgroup 0 aligns the routing while workgroups
+// 1.. quantise the activations x (they are independent), which saves a
+// dependent launch on the decode critical path. QF selects the quantiser:
+// 0 = FP8 per 128 (bf16 profile, codes + E8M0 x4), 1 = MXFP4 per 32.
+template <typename IdT, int NT, int QF>
+__global__ __launch_bounds__(NT) void moe_align_quant_kernel(const IdT* __restrict__ ids,
+                                                             const float* __restrict__ topk_w, int R, int K,
+                                                             int E, int block_m, int max_blocks,
+                                                             Dsv4AlignOut o, const uint4* __restrict__ x,
+                                                             int64_t n_groups, int rule, void* q_codes,
+                                                             void* q_scale) {
+  if (blockIdx.x == 0) {
+    align_body<IdT, NT>(ids, topk_w, R, K, E, block_m, max_blocks, o);
+    return;
+  }
+  const int64_t g = (int64_t)(blockIdx.x - 1) * NT + threadIdx.x;
+  if (QF == 0)
+    dsv4::fp8_quant_group(x, g, n_groups, nullptr, (uint2*)q_codes, nullptr, (uint32_t*)q_scale);
+  else
+    dsv4::mxfp4_quant_group(x, g, n_groups, rule, (uint32_t*)q_codes, (uint8_t*)q_scale, nullptr);
+}
+
 }  // namespace
 
 hipError_t launch_moe_align(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K, int E,
@@ -174,5 +203,30 @@ hipError_t launch_moe_align(const void* topk_ids, int ids_int64, const float* to
       hipLaunchKernelGGL((moe_align_kernel<int32_t, 1024>), dim3(1), dim3(1024), lds, st,
                          (const int32_t*)topk_ids, topk_w, R, K, E, block_m, max_blocks, o);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_align_quant(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K, int E,
+                                  int block_m, int max_blocks, const Dsv4AlignOut& o, const uint16_t* x,
+                                  int64_t n_elems, int qfmt, int rule, void* q_codes, void* q_scale,
+                                  hipStream_t st) {
+  const bool small = E <= 256 && R <= 2048;
+  const int nt = small ? 256 : 1024;
+  const size_t lds = sizeof(int) * (size_t)((E + 1) + E + E + (E + 1) + (nt / 64) * (E + 1));
+  const int64_t n_groups = n_elems / 8;
+  const int64_t qwg = (n_groups + nt - 1) / nt;
+  if (qwg + 1 > 0x7fffffffLL) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(1 + qwg));
+#define DSV4_AQ(IDT, NT_, QF)                                                                              \
+  hipLaunchKernelGGL((moe_align_quant_kernel<IDT, NT_, QF>), grid, dim3(NT_), lds, st, (const IDT*)topk_ids, \
+                     topk_w, R, K, E, block_m, max_blocks, o, (const uint4*)x, n_groups, rule, q_codes, q_scale)
+  if (small) {
+    if (ids_int64) { if (qfmt == 0) DSV4_AQ(long long, 256, 0); else DSV4_AQ(long long, 256, 1); }
+    else { if (qfmt == 0) DSV4_AQ(int32_t, 256, 0); else DSV4_AQ(int32_t, 256, 1); }
+  } else {
+    if (ids_int64) { if (qfmt == 0) DSV4_AQ(long long, 1024, 0); else DSV4_AQ(long long, 1024, 1); }
+    else { if (qfmt == 0) DSV4_AQ(int32_t, 1024, 0); else DSV4_AQ(int32_t, 1024, 1); }
+  }
+#undef DSV4_AQ
   return hipGetLastError();
 }

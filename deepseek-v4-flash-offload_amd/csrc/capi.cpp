@@ -287,16 +287,19 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
   int32_t* status = (int32_t*)(base + w.status);
   const int R = T * K;
   const int bm = w.bm;
-  int rc = dsv4_moe_align(topk_ids, ids_int64, nullptr, T, K, E, bm, w.max_blocks, sorted_ids, block_expert, npp,
-                          nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, status,
-                          stream);
-  if (rc) return rc;
+  REQUIRE(E > 0 && E <= DSV4_MAX_EXPERTS, DSV4_ERR_UNSUPPORTED, "layer: E=%d outside 1..%d", E, DSV4_MAX_EXPERTS);
+  REQUIRE(scale_rule == DSV4_RULE_CEIL_DIV6 || scale_rule == DSV4_RULE_OCP_FLOOR || profile == DSV4_PROFILE_BF16,
+          DSV4_ERR_UNSUPPORTED, "layer: unknown scale rule %d", scale_rule);
+  REQUIRE(aligned(x, 16), DSV4_ERR_SHAPE, "layer: x not 16-byte aligned");
   const bool fp8 = profile == DSV4_PROFILE_BF16;
   const int afmt = fp8 ? DSV4_AFMT_E4M3 : DSV4_AFMT_E2M1;
-  if (fp8)
-    rc = dsv4_fp8_act_quant(x, T, D, 128, nullptr, base + w.xa, nullptr, base + w.xs, stream);
-  else
-    rc = dsv4_mxfp4_act_quant(x, T, D, scale_rule, base + w.xa, base + w.xs, nullptr, stream);
+  // routing layout and the activation quantisation of x share one launch
+  Dsv4AlignOut ao{sorted_ids, block_expert, npp, nullptr, nullptr, nullptr, nullptr, nullptr,
+                  nullptr,    nullptr,      nullptr, nullptr, status};
+  int rc = hip_status(launch_moe_align_quant(topk_ids, ids_int64, nullptr, R, K, E, bm, w.max_blocks, ao,
+                                             (const uint16_t*)x, (int64_t)T * D, fp8 ? 0 : 1, scale_rule,
+                                             base + w.xa, base + w.xs, (hipStream_t)stream),
+                      "align+quant launch");
   if (rc) return rc;
   rc = dsv4_moe_gemm_gateup(afmt, base + w.xa, base + w.xs, K, sorted_ids, block_expert, npp, R, bm, w.max_blocks,
                             expert_table, D, I, topk_w, swiglu_limit, base + w.h, stream);

@@ -39,6 +39,12 @@ struct Dsv4AlignOut {
 hipError_t launch_moe_align(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K,
                             int E, int block_m, int max_blocks, const Dsv4AlignOut& o, hipStream_t st);
 
+// align (workgroup 0) and activation quantisation (workgroups 1..) in one launch;
+// qfmt 0 = FP8 per-128 codes + E8M0 x4 scales, 1 = MXFP4 per-32 (rule 0/1)
+hipError_t launch_moe_align_quant(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K, int E,
+                                  int block_m, int max_blocks, const Dsv4AlignOut& o, const uint16_t* x,
+                                  int64_t n_elems, int qfmt, int rule, void* q_codes, void* q_scale,
+                                  hipStream_t st);
 hipError_t launch_moe_gather_rows(const uint8_t* src, int64_t n_src, const int32_t* row, int64_t n_rows,
                                   int64_t row_bytes, uint8_t* dst, hipStream_t st);
 // y[t] = bf16( sum over the token's entries, ordered by key, of rows of `src` (bf16) )

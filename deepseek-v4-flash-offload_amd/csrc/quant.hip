@@ -5,6 +5,7 @@
 // so every load and store instruction of a wave covers one contiguous span.
 #include "common.h"
 #include "kernels.h"
+#include "quant_dev.h"
 
 using namespace dsv4;
 
@@ -81,116 +82,20 @@ __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint32_t* __re
 }
 
 // ---------------------------------------------------------------------------
-// act_quant (npu_ops.py:73-104): per-128 block of one row,
-//   amax = max(max|x|, 1e-4); s = 2^ceil(log2(max(amax * fp32(1/448), 2^-126)))
-//   code = e4m3fn(clamp(x / s, +-448)) (RNE); rt = bf16(e4m3(code) * s)
-// 16 lanes own one block (8 elements each).
+// Activation quantisers (bodies in quant_dev.h): one thread per 8-element group.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void fp8_act_quant_kernel(const uint4* __restrict__ x, int64_t n_groups,
                                                              uint4* __restrict__ rt, uint2* __restrict__ codes,
                                                              float* __restrict__ scale_f32,
                                                              uint32_t* __restrict__ scale_e8m0x4) {
-  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const bool live = g < n_groups;  // n_groups is a multiple of 16, so whole blocks share liveness
-  uint4 v = live ? x[g] : make_uint4(0, 0, 0, 0);
-  uint32_t w[4] = {v.x, v.y, v.z, v.w};
-  float f[8];
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = bf16_to_f32(w[i] & 0xffffu);
-    f[2 * i + 1] = bf16_to_f32(w[i] >> 16);
-    amax = fmaxf(amax, fmaxf(fabsf(f[2 * i]), fabsf(f[2 * i + 1])));
-  }
-  amax = wave_max_xor(amax, 16);
-  amax = fmaxf(amax, 1e-4f);
-  float vs = fmaxf(amax * (1.0f / 448.0f), 1.1754943508222875e-38f);
-  int k = ceil_log2(vs);
-  float s = pow2f(k), inv = pow2f(-k);
-  uint32_t c[8];
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float y = fminf(fmaxf(f[i] * inv, -448.0f), 448.0f);
-    uint32_t neg = __float_as_uint(y) >> 31;
-    uint32_t mag = e4m3_mag_code(fabsf(y));
-    c[i] = mag | (neg << 7);
-    float q = e4m3_mag_value(mag) * s;
-    uint32_t b = f32_to_bf16(neg ? -q : q);
-    if (i & 1) o[i >> 1] |= b << 16; else o[i >> 1] = b;
-  }
-  if (!live) return;
-  if (rt) rt[g] = make_uint4(o[0], o[1], o[2], o[3]);
-  if (codes) codes[g] = make_uint2(c[0] | (c[1] << 8) | (c[2] << 16) | (c[3] << 24),
-                                   c[4] | (c[5] << 8) | (c[6] << 16) | (c[7] << 24));
-  if ((threadIdx.x & 15) == 0) {
-    const int64_t blk = g >> 4;
-    if (scale_f32) scale_f32[blk] = s;
-    if (scale_e8m0x4) scale_e8m0x4[blk] = (uint32_t)(k + 127) * 0x01010101u;
-  }
+  fp8_quant_group(x, (int64_t)blockIdx.x * 256 + threadIdx.x, n_groups, rt, codes, scale_f32, scale_e8m0x4);
 }
 
-// ---------------------------------------------------------------------------
-// MXFP4 activation quant, per 32 elements; 4 lanes own one block.
-//  rule 0 "ceil_div6" (npu_ops.py:107-121):
-//     amax = max(max|x|, 6*2^-126); s = 2^ceil(log2(max(amax*fp32(1/6), 2^-126)))
-//     v = clamp(x/s, +-6); q = E2M1-RNE(|v|); sign = (v < 0); dq = bf16(+-q * s)
-//  rule 1 "ocp_floor" (OCP MX v1.0): shared = floor(log2 amax) - 2 clamped to
-//     [-127, 127] (-127 for an all-zero block); q = E2M1-RNE(min(|x|/2^shared, 6));
-//     sign = signbit(x)
-// Outputs: packed nibbles (low = even element), E8M0 scale byte, optional bf16 dq.
-// ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void mxfp4_act_quant_kernel(const uint4* __restrict__ x, int64_t n_groups,
                                                                int rule, uint32_t* __restrict__ packed,
                                                                uint8_t* __restrict__ scale,
                                                                uint4* __restrict__ dq) {
-  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const bool live = g < n_groups;  // multiple of 4
-  uint4 v = live ? x[g] : make_uint4(0, 0, 0, 0);
-  uint32_t w[4] = {v.x, v.y, v.z, v.w};
-  float f[8];
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = bf16_to_f32(w[i] & 0xffffu);
-    f[2 * i + 1] = bf16_to_f32(w[i] >> 16);
-    amax = fmaxf(amax, fmaxf(fabsf(f[2 * i]), fabsf(f[2 * i + 1])));
-  }
-  amax = wave_max_xor(amax, 4);
-  int k;
-  if (rule == 0) {
-    amax = fmaxf(amax, 6.0f * 1.1754943508222875e-38f);
-    float vs = fmaxf(amax * (1.0f / 6.0f), 1.1754943508222875e-38f);
-    k = ceil_log2(vs);
-  } else {
-    k = (amax == 0.0f) ? -127 : min(max(floor_log2(amax) - 2, -127), 127);
-  }
-  float s = pow2f(k), inv = pow2f(-k);
-  uint32_t pk = 0;
-  uint32_t o[4];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float y = f[i] * inv;
-    uint32_t neg;
-    float a;
-    if (rule == 0) {
-      y = fminf(fmaxf(y, -6.0f), 6.0f);
-      neg = (y < 0.0f) ? 1u : 0u;
-      a = fabsf(y);
-    } else {
-      neg = __float_as_uint(f[i]) >> 31;
-      a = fminf(fabsf(y), 6.0f);
-    }
-    uint32_t mag = e2m1_mag_code(a);
-    pk |= (mag | (neg << 3)) << (4 * i);
-    float q = e2m1_mag_value(mag) * s;
-    uint32_t b = f32_to_bf16(neg ? -q : q);
-    if (i & 1) o[i >> 1] |= b << 16; else o[i >> 1] = b;
-  }
-  if (!live) return;
-  packed[g] = pk;
-  if (dq) dq[g] = make_uint4(o[0], o[1], o[2], o[3]);
-  if ((threadIdx.x & 3) == 0) scale[g >> 2] = (uint8_t)(k + 127);
+  mxfp4_quant_group(x, (int64_t)blockIdx.x * 256 + threadIdx.x, n_groups, rule, packed, scale, dq);
 }
 
 // ---------------------------------------------------------------------------
