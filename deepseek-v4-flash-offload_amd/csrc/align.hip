@@ -174,9 +174,9 @@ __global__ __launch_bounds__(NT) void moe_align_quant_kernel(const IdT* __restri
   }
   const int64_t g = (int64_t)(blockIdx.x - 1) * NT + threadIdx.x;
   if (QF == 0)
-    dsv4::fp8_quant_group(x, g, n_groups, nullptr, (uint2*)q_codes, nullptr, (uint32_t*)q_scale);
+    dsv4::fp8_quant_group(x, g, g < n_groups, nullptr, (uint2*)q_codes, nullptr, (uint32_t*)q_scale);
   else
-    dsv4::mxfp4_quant_group(x, g, n_groups, rule, (uint32_t*)q_codes, (uint8_t*)q_scale, nullptr);
+    dsv4::mxfp4_quant_group(x, g, g < n_groups, rule, (uint32_t*)q_codes, (uint8_t*)q_scale, nullptr);
 }
 
 }  // namespace

@@ -221,8 +221,13 @@ int dsv4_moe_gemm_down(int afmt, const void* a, const void* a_scale, const int32
 }
 
 // ---------------------------------------------------------------------------
-// Fused routed layer: align -> activation quant -> gate/up GEMM + SwiGLU ->
-// h quant -> down GEMM -> combine. Workspace regions are 256-byte aligned.
+// Fused routed layer: [align | quantise x] -> gate/up GEMM + SwiGLU (+ quantise
+// h in the epilogue where a wave or workgroup holds whole quantisation blocks:
+// MXFP4 always, FP8 in the 64/128-row kernel; a separate FP8 quantisation
+// launch for 16-row blocks) -> down GEMM -> combine. No step needs ordering
+// between workgroups of one launch: device-scope fences for such hand-offs were
+// measured to cost far more than the launches they would save. Workspace
+// regions are 256-byte aligned.
 struct LayerWs {
   int64_t sorted_ids, block_expert, npp, status, xa, xs, h, ha, hs, out, total;
   int max_blocks;
@@ -301,16 +306,59 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
                                              base + w.xa, base + w.xs, (hipStream_t)stream),
                       "align+quant launch");
   if (rc) return rc;
-  rc = dsv4_moe_gemm_gateup(afmt, base + w.xa, base + w.xs, K, sorted_ids, block_expert, npp, R, bm, w.max_blocks,
-                            expert_table, D, I, topk_w, swiglu_limit, base + w.h, stream);
+  REQUIRE(moe_gemm_supported_kdim(D) && moe_gemm_supported_kdim(I), DSV4_ERR_UNSUPPORTED,
+          "layer: no GEMM compiled for D=%d / I=%d", D, I);
+  const Dsv4ExpertPtrs* table = (const Dsv4ExpertPtrs*)expert_table;
+  // gate/up + SwiGLU, quantising h in the epilogue where the kernel holds whole blocks
+  const bool hq_fused = !fp8 || bm != DSV4_GEMM_BLOCK_M;
+  Dsv4GemmArgs gu{};
+  gu.afmt = afmt;
+  gu.a = (const uint8_t*)(base + w.xa);
+  gu.a_row_bytes = fp8 ? (int64_t)D : (int64_t)D / 2;
+  gu.a_scale = (const uint8_t*)(base + w.xs);
+  gu.a_row_div = K;
+  gu.sorted_ids = sorted_ids;
+  gu.block_expert = block_expert;
+  gu.num_post_padded = npp;
+  gu.R = R;
+  gu.block_m = bm;
+  gu.max_blocks = w.max_blocks;
+  gu.experts = table;
+  gu.Kdim = D;
+  gu.N = I;
+  gu.topk_w = topk_w;
+  gu.swiglu_limit = swiglu_limit;
+  gu.out = (uint16_t*)(base + w.h);
+  if (hq_fused) {
+    gu.hq_mode = fp8 ? 1 : 2;
+    gu.hq_rule = scale_rule;
+    gu.hq_skip_h = 1;
+    gu.hq_codes = (uint8_t*)(base + w.ha);
+    gu.hq_scale = (uint8_t*)(base + w.hs);
+  }
+  rc = hip_status(launch_moe_gemm_gateup(gu, (hipStream_t)stream), "gemm gate/up launch");
   if (rc) return rc;
-  if (fp8)
+  if (!hq_fused) {  // FP8 blocks of 128 columns span four single-wave workgroups
     rc = dsv4_fp8_act_quant(base + w.h, R, I, 128, nullptr, base + w.ha, nullptr, base + w.hs, stream);
-  else
-    rc = dsv4_mxfp4_act_quant(base + w.h, R, I, scale_rule, base + w.ha, base + w.hs, nullptr, stream);
-  if (rc) return rc;
-  rc = dsv4_moe_gemm_down(afmt, base + w.ha, base + w.hs, sorted_ids, block_expert, npp, R, bm, w.max_blocks,
-                          expert_table, I, D, base + w.out, stream);
+    if (rc) return rc;
+  }
+  Dsv4GemmArgs dn{};
+  dn.afmt = afmt;
+  dn.a = (const uint8_t*)(base + w.ha);
+  dn.a_row_bytes = fp8 ? (int64_t)I : (int64_t)I / 2;
+  dn.a_scale = (const uint8_t*)(base + w.hs);
+  dn.a_row_div = 1;
+  dn.sorted_ids = sorted_ids;
+  dn.block_expert = block_expert;
+  dn.num_post_padded = npp;
+  dn.R = R;
+  dn.block_m = bm;
+  dn.max_blocks = w.max_blocks;
+  dn.experts = table;
+  dn.Kdim = I;
+  dn.N = D;
+  dn.out = (uint16_t*)(base + w.out);
+  rc = hip_status(launch_moe_gemm_down(dn, (hipStream_t)stream), "gemm down launch");
   if (rc) return rc;
   return dsv4_moe_combine(base + w.out, topk_ids, ids_int64, T, K, D, y, stream);
 }

@@ -38,6 +38,7 @@
 //   C       : lane l holds C[4*(l/16)+i][l%16], i = 0..3.
 #include "common.h"
 #include "kernels.h"
+#include "quant_dev.h"
 
 namespace {
 
@@ -199,12 +200,16 @@ DSV4_DEV void compute(v4f* acc, const AStage<AFMT>& a, const BStage& b) {
 }
 
 // Epilogue of one 16-row subtile: lane holds rows row0 + 4*g + i (i = 0..3) of
-// column r16 of each of the 4 tiles.
+// column r16 of each of the 4 tiles. Gate/up: hb receives the bf16 h values the
+// SwiGLU produced (tiles t = 0, 1 are intermediate columns col0 + 16 t + r16) and
+// fr the rows' flat indices; h is written unless the caller fuses its quantisation.
 template <bool GATEUP>
-DSV4_DEV void store_tile(const Dsv4GemmArgs& p, const v4f* acc, int row0, int col0, int g, int r16) {
+DSV4_DEV void store_tile(const Dsv4GemmArgs& p, const v4f* acc, int row0, int col0, int g, int r16,
+                         uint32_t (*hb)[2] = nullptr, int* fr = nullptr) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int f = p.sorted_ids[row0 + 4 * g + i];
+    if (fr) fr[i] = f;
     if (f >= p.R) continue;
     uint16_t* orow = p.out + (int64_t)f * p.N + col0 + r16;
     if (GATEUP) {
@@ -219,11 +224,39 @@ DSV4_DEV void store_tile(const Dsv4GemmArgs& p, const v4f* acc, int row0, int co
           gt = fminf(gt, p.swiglu_limit);
         }
         const float h = gt / (1.0f + expf(-gt)) * up * w;
-        orow[16 * t] = (uint16_t)dsv4::f32_to_bf16(h);
+        const uint32_t b = dsv4::f32_to_bf16(h);
+        if (hb) hb[i][t] = b;
+        if (!p.hq_skip_h) orow[16 * t] = (uint16_t)b;
       }
     } else {
 #pragma unroll
       for (int t = 0; t < kNT; ++t) orow[16 * t] = (uint16_t)dsv4::f32_to_bf16(acc[t][i]);
+    }
+  }
+}
+
+// MXFP4 quantisation of the h subtile a gate/up wave holds: its 32 intermediate
+// columns are exactly one 32-element block of each row, spread over the 16
+// lanes of lane group g (2 values each). Same arithmetic as mxfp4_quant_group.
+DSV4_DEV void quantise_h_mxfp4(const Dsv4GemmArgs& p, const uint32_t (*hb)[2], const int* fr, int col0, int g,
+                               int r16) {
+  (void)g;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float v0 = dsv4::bf16_to_f32(hb[i][0]), v1 = dsv4::bf16_to_f32(hb[i][1]);
+    const float amax = dsv4::wave_max_xor(fmaxf(fabsf(v0), fabsf(v1)), 16);
+    const int k = dsv4::mxfp4_block_exp(amax, p.hq_rule);
+    const float inv = dsv4::pow2f(-k);
+    const uint32_t n0 = dsv4::mxfp4_nibble(v0, inv, p.hq_rule), n1 = dsv4::mxfp4_nibble(v1, inv, p.hq_rule);
+    const uint32_t o0 = (uint32_t)__shfl_xor((int)n0, 1, 64), o1 = (uint32_t)__shfl_xor((int)n1, 1, 64);
+    const int f = fr[i];
+    if (f < p.R) {
+      uint8_t* row = p.hq_codes + (int64_t)f * (p.N / 2) + col0 / 2;
+      if ((r16 & 1) == 0) {  // low nibble = even column
+        row[r16 / 2] = (uint8_t)(n0 | (o0 << 4));
+        row[8 + r16 / 2] = (uint8_t)(n1 | (o1 << 4));
+      }
+      if (r16 == 0) p.hq_scale[(int64_t)f * (p.N / 32) + col0 / 32] = (uint8_t)(k + 127);
     }
   }
 }
@@ -308,7 +341,14 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
     }
   }
 
-  store_tile<GATEUP>(p, acc, mb * kBM, col0, g, r16);
+  if (GATEUP && p.hq_mode == 2) {  // MXFP4 h: this wave holds whole 32-column blocks
+    uint32_t hb[4][2];
+    int fr[4];
+    store_tile<GATEUP>(p, acc, mb * kBM, col0, g, r16, hb, fr);
+    quantise_h_mxfp4(p, hb, fr, col0, g, r16);
+  } else {
+    store_tile<GATEUP>(p, acc, mb * kBM, col0, g, r16);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -464,8 +504,48 @@ __global__ __launch_bounds__(256, (MT <= 4 ? 2 : 1)) void moe_gemm_tiled_kernel(
     }
   }
 
+  if (GATEUP && p.hq_mode) {
+    uint32_t hb[MT][4][2];
+    int fr[MT][4];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) store_tile<GATEUP>(p, acc[mt], mb * BM + 16 * mt, col0, g, r16);
+    for (int mt = 0; mt < MT; ++mt) store_tile<GATEUP>(p, acc[mt], mb * BM + 16 * mt, col0, g, r16, hb[mt], fr[mt]);
+    if (p.hq_mode == 2) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) quantise_h_mxfp4(p, hb[mt], fr[mt], col0, g, r16);
+    } else {
+      // FP8 per 128: the workgroup's four waves hold the 128 columns of each row;
+      // row maxima meet in LDS (the K loop is done with a_lds)
+      float* am = (float*)&a_lds[0][0];  // [4 waves][BM rows]
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float m = dsv4::wave_max_xor(
+              fmaxf(fabsf(dsv4::bf16_to_f32(hb[mt][i][0])), fabsf(dsv4::bf16_to_f32(hb[mt][i][1]))), 16);
+          if (r16 == 0) am[wave * BM + 16 * mt + 4 * g + i] = m;
+        }
+      __syncthreads();
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = 16 * mt + 4 * g + i, f = fr[mt][i];
+          const float amax = fmaxf(fmaxf(am[row], am[BM + row]), fmaxf(am[2 * BM + row], am[3 * BM + row]));
+          const int k = dsv4::fp8_block_exp(amax);
+          const float inv = dsv4::pow2f(-k);
+          if (f < p.R) {
+            uint8_t* crow = p.hq_codes + (int64_t)f * p.N + col0 + r16;
+            crow[0] = (uint8_t)dsv4::fp8_code(dsv4::bf16_to_f32(hb[mt][i][0]), inv);
+            crow[16] = (uint8_t)dsv4::fp8_code(dsv4::bf16_to_f32(hb[mt][i][1]), inv);
+            if (wave == 0 && r16 == 0)
+              *(uint32_t*)(p.hq_scale + (int64_t)f * (p.N / 32) + (col0 & ~127) / 32) = (uint32_t)(k + 127) * 0x01010101u;
+          }
+        }
+    }
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) store_tile<GATEUP>(p, acc[mt], mb * BM + 16 * mt, col0, g, r16);
+  }
 }
 
 }  // namespace

@@ -73,7 +73,16 @@ struct Dsv4GemmArgs {
   int N;                          // output columns (I for gate/up, D for down)
   const float* topk_w;            // [R] routing weight by flat index (gate/up only)
   float swiglu_limit;             // <= 0 disables the clamp
-  uint16_t* out;                  // bf16 [R, N] by flat index
+  uint16_t* out;                  // bf16 [R, N] by flat index (gate/up: h, may be skipped, see hq_mode)
+  // ---- gate/up only: quantise h for the down GEMM in the epilogue (zero = off).
+  //   hq_mode 1: FP8 per 128 (codes [R, N] + E8M0 x4 [R, N/32]); only where a workgroup
+  //   holds all 128 columns of a block (block_m 64/128 kernels). 2: MXFP4 per 32 with rule
+  //   hq_rule (packed [R, N/2] + E8M0 [R, N/32]). hq_skip_h: do not write the bf16 h.
+  int hq_mode;
+  int hq_rule;
+  int hq_skip_h;
+  uint8_t* hq_codes;
+  uint8_t* hq_scale;
 };
 hipError_t launch_moe_gemm_gateup(const Dsv4GemmArgs& a, hipStream_t st);
 hipError_t launch_moe_gemm_down(const Dsv4GemmArgs& a, hipStream_t st);

@@ -88,14 +88,16 @@ __global__ __launch_bounds__(256) void fp8_act_quant_kernel(const uint4* __restr
                                                              uint4* __restrict__ rt, uint2* __restrict__ codes,
                                                              float* __restrict__ scale_f32,
                                                              uint32_t* __restrict__ scale_e8m0x4) {
-  fp8_quant_group(x, (int64_t)blockIdx.x * 256 + threadIdx.x, n_groups, rt, codes, scale_f32, scale_e8m0x4);
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  fp8_quant_group(x, g, g < n_groups, rt, codes, scale_f32, scale_e8m0x4);  // n_groups % 16 == 0
 }
 
 __global__ __launch_bounds__(256) void mxfp4_act_quant_kernel(const uint4* __restrict__ x, int64_t n_groups,
                                                                int rule, uint32_t* __restrict__ packed,
                                                                uint8_t* __restrict__ scale,
                                                                uint4* __restrict__ dq) {
-  mxfp4_quant_group(x, (int64_t)blockIdx.x * 256 + threadIdx.x, n_groups, rule, packed, scale, dq);
+  const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  mxfp4_quant_group(x, g, g < n_groups, rule, packed, scale, dq);  // n_groups % 4 == 0
 }
 
 // ---------------------------------------------------------------------------

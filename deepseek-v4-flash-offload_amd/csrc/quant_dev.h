@@ -13,10 +13,24 @@ namespace dsv4 {
 // act_quant (npu_ops.py:73-104): per-128 block of one row,
 //   amax = max(max|x|, 1e-4); s = 2^ceil(log2(max(amax * fp32(1/448), 2^-126)))
 //   code = e4m3fn(clamp(x / s, +-448)) (RNE); rt = bf16(e4m3(code) * s)
-DSV4_DEV void fp8_quant_group(const uint4* __restrict__ x, int64_t g, int64_t n_groups, uint4* __restrict__ rt,
+// block exponent k of a 128-element FP8 block with abs-max amax (scale 2^k)
+DSV4_DEV int fp8_block_exp(float amax) {
+  amax = fmaxf(amax, 1e-4f);
+  float vs = fmaxf(amax * (1.0f / 448.0f), 1.1754943508222875e-38f);
+  return ceil_log2(vs);
+}
+
+// E4M3fn code of element f of a block with inverse scale inv = 2^-k
+DSV4_DEV uint32_t fp8_code(float f, float inv) {
+  float y = fminf(fmaxf(f * inv, -448.0f), 448.0f);
+  uint32_t neg = __float_as_uint(y) >> 31;
+  return e4m3_mag_code(fabsf(y)) | (neg << 7);
+}
+
+// `live` must be the same for the 16 lanes of a block.
+DSV4_DEV void fp8_quant_group(const uint4* __restrict__ x, int64_t g, bool live, uint4* __restrict__ rt,
                               uint2* __restrict__ codes, float* __restrict__ scale_f32,
                               uint32_t* __restrict__ scale_e8m0x4) {
-  const bool live = g < n_groups;  // n_groups is a multiple of 16, so whole blocks share liveness
   uint4 v = live ? x[g] : make_uint4(0, 0, 0, 0);
   uint32_t w[4] = {v.x, v.y, v.z, v.w};
   float f[8];
@@ -28,18 +42,14 @@ DSV4_DEV void fp8_quant_group(const uint4* __restrict__ x, int64_t g, int64_t n_
     amax = fmaxf(amax, fmaxf(fabsf(f[2 * i]), fabsf(f[2 * i + 1])));
   }
   amax = wave_max_xor(amax, 16);
-  amax = fmaxf(amax, 1e-4f);
-  float vs = fmaxf(amax * (1.0f / 448.0f), 1.1754943508222875e-38f);
-  int k = ceil_log2(vs);
+  const int k = fp8_block_exp(amax);
   float s = pow2f(k), inv = pow2f(-k);
   uint32_t c[8];
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    float y = fminf(fmaxf(f[i] * inv, -448.0f), 448.0f);
-    uint32_t neg = __float_as_uint(y) >> 31;
-    uint32_t mag = e4m3_mag_code(fabsf(y));
-    c[i] = mag | (neg << 7);
+    c[i] = fp8_code(f[i], inv);
+    const uint32_t neg = c[i] >> 7, mag = c[i] & 0x7fu;
     float q = e4m3_mag_value(mag) * s;
     uint32_t b = f32_to_bf16(neg ? -q : q);
     if (i & 1) o[i >> 1] |= b << 16; else o[i >> 1] = b;
@@ -63,10 +73,36 @@ DSV4_DEV void fp8_quant_group(const uint4* __restrict__ x, int64_t g, int64_t n_
 //     [-127, 127] (-127 for an all-zero block); q = E2M1-RNE(min(|x|/2^shared, 6));
 //     sign = signbit(x)
 // Outputs: packed nibbles (low = even element), E8M0 scale byte, optional bf16 dq.
-DSV4_DEV void mxfp4_quant_group(const uint4* __restrict__ x, int64_t g, int64_t n_groups, int rule,
+// shared exponent of an MXFP4 block with abs-max `amax` (rule 0 / 1 as above)
+DSV4_DEV int mxfp4_block_exp(float amax, int rule) {
+  if (rule == 0) {
+    amax = fmaxf(amax, 6.0f * 1.1754943508222875e-38f);
+    float vs = fmaxf(amax * (1.0f / 6.0f), 1.1754943508222875e-38f);
+    return ceil_log2(vs);
+  }
+  return (amax == 0.0f) ? -127 : min(max(floor_log2(amax) - 2, -127), 127);
+}
+
+// sign-magnitude E2M1 nibble of element f of a block with inverse scale inv = 2^-k
+DSV4_DEV uint32_t mxfp4_nibble(float f, float inv, int rule) {
+  float y = f * inv;
+  uint32_t neg;
+  float a;
+  if (rule == 0) {
+    y = fminf(fmaxf(y, -6.0f), 6.0f);
+    neg = (y < 0.0f) ? 1u : 0u;
+    a = fabsf(y);
+  } else {
+    neg = __float_as_uint(f) >> 31;
+    a = fminf(fabsf(y), 6.0f);
+  }
+  return e2m1_mag_code(a) | (neg << 3);
+}
+
+// `live` must be the same for the 4 lanes of a block.
+DSV4_DEV void mxfp4_quant_group(const uint4* __restrict__ x, int64_t g, bool live, int rule,
                                 uint32_t* __restrict__ packed, uint8_t* __restrict__ scale,
                                 uint4* __restrict__ dq) {
-  const bool live = g < n_groups;  // multiple of 4
   uint4 v = live ? x[g] : make_uint4(0, 0, 0, 0);
   uint32_t w[4] = {v.x, v.y, v.z, v.w};
   float f[8];
@@ -78,32 +114,15 @@ DSV4_DEV void mxfp4_quant_group(const uint4* __restrict__ x, int64_t g, int64_t 
     amax = fmaxf(amax, fmaxf(fabsf(f[2 * i]), fabsf(f[2 * i + 1])));
   }
   amax = wave_max_xor(amax, 4);
-  int k;
-  if (rule == 0) {
-    amax = fmaxf(amax, 6.0f * 1.1754943508222875e-38f);
-    float vs = fmaxf(amax * (1.0f / 6.0f), 1.1754943508222875e-38f);
-    k = ceil_log2(vs);
-  } else {
-    k = (amax == 0.0f) ? -127 : min(max(floor_log2(amax) - 2, -127), 127);
-  }
+  const int k = mxfp4_block_exp(amax, rule);
   float s = pow2f(k), inv = pow2f(-k);
   uint32_t pk = 0;
   uint32_t o[4];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    float y = f[i] * inv;
-    uint32_t neg;
-    float a;
-    if (rule == 0) {
-      y = fminf(fmaxf(y, -6.0f), 6.0f);
-      neg = (y < 0.0f) ? 1u : 0u;
-      a = fabsf(y);
-    } else {
-      neg = __float_as_uint(f[i]) >> 31;
-      a = fminf(fabsf(y), 6.0f);
-    }
-    uint32_t mag = e2m1_mag_code(a);
-    pk |= (mag | (neg << 3)) << (4 * i);
+    const uint32_t nib = mxfp4_nibble(f[i], inv, rule);
+    pk |= nib << (4 * i);
+    const uint32_t neg = nib >> 3, mag = nib & 7u;
     float q = e2m1_mag_value(mag) * s;
     uint32_t b = f32_to_bf16(neg ? -q : q);
     if (i & 1) o[i >> 1] |= b << 16; else o[i >> 1] = b;
