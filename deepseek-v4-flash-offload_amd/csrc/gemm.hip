@@ -394,16 +394,18 @@ DSV4_DEV void compute_tiled(v4f (*acc)[kNT], const uint8_t* lds, const uint8_t* 
   }
 }
 
-template <int AFMT, bool GATEUP, int NST, int MT>
-__global__ __launch_bounds__(256, (MT <= 4 ? 2 : 1)) void moe_gemm_tiled_kernel(Dsv4GemmArgs p) {
+template <int AFMT, bool GATEUP, int NST, int MT, int NW>
+__global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gemm_tiled_kernel(Dsv4GemmArgs p) {
   constexpr int BM = 16 * MT;
+  constexpr int NTH = 64 * NW;                // threads per workgroup
   constexpr int ASB = AFMT == 0 ? 256 : 128;  // A bytes per row per stage
   constexpr int AROW = ASB + 16;              // padded LDS row stride
-  constexpr int LV = BM * ASB / (256 * 16);   // 16-byte A chunks one thread moves per stage
+  constexpr int LV = BM * ASB / (NTH * 16);   // 16-byte A chunks one thread moves per stage
   constexpr int KSB = 8 * NST;                // scale bytes per row (K / 32)
   constexpr int ASP = KSB + 16;               // A scale table pitch: 16 rows on distinct banks
   constexpr int AS_CHUNKS = BM * KSB / 16;
-  static_assert(LV >= 1 && LV * 256 * 16 == BM * ASB, "loader granularity");
+  static_assert(LV >= 1 && LV * NTH * 16 == BM * ASB, "loader granularity");
+  static_assert(NW % 4 == 0, "four gate/up waves make one 128-column FP8 block");
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][BM * AROW];
   __shared__ __attribute__((aligned(16))) uint8_t as_tab[BM * ASP];
 
@@ -417,13 +419,13 @@ __global__ __launch_bounds__(256, (MT <= 4 ? 2 : 1)) void moe_gemm_tiled_kernel(
 
   // loader role: load v of wave w moves 1 KB of the stage's A tile = whole
   // 128-byte lines (4 rows x 256 B for E4M3, 8 rows x 128 B for E2M1), so each
-  // line is one L1->L2 request; lane L carries 16-byte chunk (v*4 + w)*64 + L
+  // line is one L1->L2 request; lane L carries 16-byte chunk (v*NW + w)*64 + L
   constexpr int CPRW = ASB / 16;  // 16-byte chunks per A row per stage
   const uint8_t* lsrc[LV];
   int ldst[LV];
 #pragma unroll
   for (int v = 0; v < LV; ++v) {
-    const int id = (v * 4 + wave) * 64 + lane, row = id / CPRW, ch = id % CPRW;
+    const int id = (v * NW + wave) * 64 + lane, row = id / CPRW, ch = id % CPRW;
     const int f = p.sorted_ids[mb * BM + row];
     const int64_t ar = f < p.R ? (int64_t)(f / p.a_row_div) : 0;  // padding rows read row 0
     lsrc[v] = p.a + ar * p.a_row_bytes + 16 * ch;
@@ -435,7 +437,7 @@ __global__ __launch_bounds__(256, (MT <= 4 ? 2 : 1)) void moe_gemm_tiled_kernel(
   const uint8_t* bt[kNT];
   const uint8_t* bst[kNT];
   if (GATEUP) {
-    col0 = blockIdx.x * 128 + wave * 32;
+    col0 = blockIdx.x * (NW * 32) + wave * 32;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int64_t row = col0 + 16 * t + r16;
@@ -445,7 +447,7 @@ __global__ __launch_bounds__(256, (MT <= 4 ? 2 : 1)) void moe_gemm_tiled_kernel(
       bst[t + 2] = ex.w3s + row * bsrow;
     }
   } else {
-    col0 = blockIdx.x * 256 + wave * 64;
+    col0 = blockIdx.x * (NW * 64) + wave * 64;
 #pragma unroll
     for (int t = 0; t < kNT; ++t) {
       const int64_t row = col0 + 16 * t + r16;
@@ -467,8 +469,8 @@ __global__ __launch_bounds__(256, (MT <= 4 ? 2 : 1)) void moe_gemm_tiled_kernel(
 #pragma unroll
     for (int t = 0; t < kNT; ++t) load_row_scales<NST>(bs_row[t], bst[t], g);
 #pragma unroll
-    for (int i = 0; i < (AS_CHUNKS + 255) / 256; ++i) {
-      const int c = i * 256 + tid;
+    for (int i = 0; i < (AS_CHUNKS + NTH - 1) / NTH; ++i) {
+      const int c = i * NTH + tid;
       if (c < AS_CHUNKS) {
         const int row = c / (KSB / 16), ch = c % (KSB / 16);
         const int f = p.sorted_ids[mb * BM + row];
@@ -513,9 +515,9 @@ __global__ __launch_bounds__(256, (MT <= 4 ? 2 : 1)) void moe_gemm_tiled_kernel(
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) quantise_h_mxfp4(p, hb[mt], fr[mt], col0, g, r16);
     } else {
-      // FP8 per 128: the workgroup's four waves hold the 128 columns of each row;
+      // FP8 per 128: waves 4b..4b+3 hold the 128 columns of block b of each row;
       // row maxima meet in LDS (the K loop is done with a_lds)
-      float* am = (float*)&a_lds[0][0];  // [4 waves][BM rows]
+      float* am = (float*)&a_lds[0][0];  // [NW waves][BM rows]
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -530,14 +532,15 @@ __global__ __launch_bounds__(256, (MT <= 4 ? 2 : 1)) void moe_gemm_tiled_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int row = 16 * mt + 4 * g + i, f = fr[mt][i];
-          const float amax = fmaxf(fmaxf(am[row], am[BM + row]), fmaxf(am[2 * BM + row], am[3 * BM + row]));
+          const float* ab = am + (wave & ~3) * BM + row;
+          const float amax = fmaxf(fmaxf(ab[0], ab[BM]), fmaxf(ab[2 * BM], ab[3 * BM]));
           const int k = dsv4::fp8_block_exp(amax);
           const float inv = dsv4::pow2f(-k);
           if (f < p.R) {
             uint8_t* crow = p.hq_codes + (int64_t)f * p.N + col0 + r16;
             crow[0] = (uint8_t)dsv4::fp8_code(dsv4::bf16_to_f32(hb[mt][i][0]), inv);
             crow[16] = (uint8_t)dsv4::fp8_code(dsv4::bf16_to_f32(hb[mt][i][1]), inv);
-            if (wave == 0 && r16 == 0)
+            if ((wave & 3) == 0 && r16 == 0)
               *(uint32_t*)(p.hq_scale + (int64_t)f * (p.N / 32) + (col0 & ~127) / 32) = (uint32_t)(k + 127) * 0x01010101u;
           }
         }
@@ -561,17 +564,19 @@ static void launch_nst(const Dsv4GemmArgs& a, hipStream_t st) {
       hipLaunchKernelGGL((moe_gemm_kernel<1, GATEUP, NST>), grid, dim3(64 * kWaves), 0, st, a);
     return;
   }
+  // 4-wave workgroups (8-wave ones, sharing each A tile across twice the
+  // columns, measured no faster)
   const dim3 grid(a.N / (4 * cols_per_wave), a.max_blocks);
   if (a.block_m == 64) {
     if (a.afmt == 0)
-      hipLaunchKernelGGL((moe_gemm_tiled_kernel<0, GATEUP, NST, 4>), grid, dim3(256), 0, st, a);
+      hipLaunchKernelGGL((moe_gemm_tiled_kernel<0, GATEUP, NST, 4, 4>), grid, dim3(256), 0, st, a);
     else
-      hipLaunchKernelGGL((moe_gemm_tiled_kernel<1, GATEUP, NST, 4>), grid, dim3(256), 0, st, a);
+      hipLaunchKernelGGL((moe_gemm_tiled_kernel<1, GATEUP, NST, 4, 4>), grid, dim3(256), 0, st, a);
   } else {
     if (a.afmt == 0)
-      hipLaunchKernelGGL((moe_gemm_tiled_kernel<0, GATEUP, NST, 8>), grid, dim3(256), 0, st, a);
+      hipLaunchKernelGGL((moe_gemm_tiled_kernel<0, GATEUP, NST, 8, 4>), grid, dim3(256), 0, st, a);
     else
-      hipLaunchKernelGGL((moe_gemm_tiled_kernel<1, GATEUP, NST, 8>), grid, dim3(256), 0, st, a);
+      hipLaunchKernelGGL((moe_gemm_tiled_kernel<1, GATEUP, NST, 8, 4>), grid, dim3(256), 0, st, a);
   }
 }
 

@@ -25,7 +25,7 @@ extern "C" {
 
 #define DSV4_MAX_EXPERTS 512
 #define DSV4_MAX_TOPK 32
-#define DSV4_GEMM_BLOCK_M 16
+#define DSV4_GEMM_BLOCK_M 16 /* rows per M block for decode-sized calls; the GEMMs also take 64 and 128 */
 
 /* activation formats of the grouped GEMM A operand */
 #define DSV4_AFMT_E4M3 0 /* one E4M3fn code per byte, E8M0 per 32 (bf16 profile) */
@@ -127,7 +127,10 @@ int dsv4_moe_combine(const void* out_flat, const void* topk_ids, int ids_int64, 
  * Replaces the two npu_grouped_matmul calls of deepseek_v4.py:177-182
  * (afmt E4M3) / 231-232 (afmt E2M1). A rows are gathered on load: padded slot
  * p reads A row sorted_ids[p] / a_row_div. a: [rows, D] codes (E4M3) or
- * [rows, D/2] (E2M1), a_scale [rows, D/32]. h_out: bf16 [R, I] by flat index. */
+ * [rows, D/2] (E2M1), a_scale [rows, D/32]. h_out: bf16 [R, I] by flat index.
+ * block_m (the moe_align block size) is 16 (single-wave workgroups, decode),
+ * 64 or 128 (LDS-tiled workgroups: each weight fragment serves 4 or 8 row
+ * tiles); D and I must be 256 * 2^n (512..8192) and I a multiple of 128. */
 int dsv4_moe_gemm_gateup(int afmt, const void* a, const void* a_scale, int a_row_div, const int32_t* sorted_ids,
                          const int32_t* block_expert, const int32_t* num_post_padded, int R, int block_m,
                          int max_blocks, const void* expert_table, int D, int I, const float* topk_w,
@@ -144,8 +147,12 @@ int dsv4_moe_gemm_down(int afmt, const void* a, const void* a_scale, const int32
  * OffloadDeepseekV4MoE._routed (deepseek_v4.py:150-197, profile BF16) or
  * _routed_mxfp4 (deepseek_v4.py:199-245, profile A4W4) after routing:
  * moe_align -> activation quant -> gate/up GEMM + SwiGLU -> h quant -> down
- * GEMM -> combine. x [T, D] bf16, topk_ids/topk_w [T, K], y [T, D] bf16.
- * scale_rule applies to the A4W4 profile only. */
+ * GEMM -> combine, as 4-5 launches on `stream` (align and the quantisation of
+ * x share one; h is quantised in the gate/up epilogue except for the FP8
+ * profile below 2048 routed rows). M blocks of 16 rows below 2048 routed rows,
+ * 64 from there on. x [T, D] bf16, topk_ids/topk_w [T, K], y [T, D] bf16.
+ * scale_rule applies to the A4W4 profile only. The workspace (size from
+ * dsv4_moe_layer_workspace_bytes, 256-byte aligned) needs no initialisation. */
 int dsv4_moe_layer_workspace_bytes(int T, int K, int E, int D, int I, int profile, int64_t* bytes);
 int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
                            const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
