@@ -68,12 +68,25 @@ def _expert_f32(experts, e):
             Q.dequant_fp4_weight_f32(ex["w2p"], ex["w2s"]))
 
 
+def _map(fn, items, workers):
+    """``list(map(fn, items))``, on a thread pool when ``workers > 1`` (the
+    per-expert numpy work releases the GIL; results do not depend on it)."""
+    if workers <= 1 or len(items) <= 1:
+        return [fn(i) for i in items]
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(max_workers=workers) as ex:
+        return list(ex.map(fn, items))
+
+
 def routed_bf16(x_bf16, topk_ids, topk_w, experts, n_experts=256, swiglu_limit=10.0,
-                fp8_act=True):
+                fp8_act=True, workers=1):
     """bf16 profile of ``_routed``. Returns a dict of every intermediate.
 
     ``experts[e]`` holds the packed checkpoint tensors ``w{1,2,3}{p,s}``
-    (``[N, K/2]`` uint8 + ``[N, K/32]`` UE8M0 bytes)."""
+    (``[N, K/2]`` uint8 + ``[N, K/32]`` UE8M0 bytes). ``workers`` runs the
+    per-expert dequant and GEMMs on that many host threads (the reference's CPU
+    path uses every core, ``ds4_npu_moe.py``); each expert's rows are computed
+    the same way either way."""
     x_bf16 = np.asarray(x_bf16, np.uint16)
     T = x_bf16.shape[0]
     al = moe_align(topk_ids, topk_w, n_experts)
@@ -84,23 +97,30 @@ def routed_bf16(x_bf16, topk_ids, topk_w, experts, n_experts=256, swiglu_limit=1
     D = x_bf16.shape[1]
     gate = np.zeros((R, I), np.float32)
     up = np.zeros((R, I), np.float32)
-    o = 0
+    starts = np.concatenate([[0], np.cumsum(al["group_list"])]).astype(np.int64)
+    groups = [(int(e), int(starts[i]), int(starts[i + 1]))
+              for i, e in enumerate(al["active"])]
     W = {}
-    for e, c in zip(al["active"], al["group_list"]):
-        W[int(e)] = _expert_f32(experts, e)
-        w1, w3, _ = W[int(e)]
-        gate[o:o + c] = Q.f32_to_bf16_f32(matmul_nt(x_sorted[o:o + c], w1))   # :177-179
-        up[o:o + c] = Q.f32_to_bf16_f32(matmul_nt(x_sorted[o:o + c], w3))     # :180-182
-        o += c
+
+    def gate_up(g):
+        e, a, b = g
+        W[e] = _expert_f32(experts, e)
+        w1, w3, _ = W[e]
+        gate[a:b] = Q.f32_to_bf16_f32(matmul_nt(x_sorted[a:b], w1))   # :177-179
+        up[a:b] = Q.f32_to_bf16_f32(matmul_nt(x_sorted[a:b], w3))     # :180-182
+
+    _map(gate_up, groups, workers)
     h = swiglu(gate, up, al["s_w"], swiglu_limit)                        # :184-187
     h_bf16 = Q.f32_to_bf16_bits(h)
     hq = Q.act_quant(h_bf16, 128)[0] if fp8_act else h_bf16             # :188
     hq_f = Q.bf16_bits_to_f32(hq)
     out = np.zeros((R, D), np.float32)
-    o = 0
-    for e, c in zip(al["active"], al["group_list"]):
-        out[o:o + c] = matmul_nt(hq_f[o:o + c], W[int(e)][2])           # :191-193
-        o += c
+
+    def down(g):
+        e, a, b = g
+        out[a:b] = matmul_nt(hq_f[a:b], W[e][2])                        # :191-193
+
+    _map(down, groups, workers)
     out_bf16 = Q.f32_to_bf16_bits(out)
     y = unpermute(out_bf16, al["row"], T)                                # :195-197
     return {"align": al, "xq": xq, "gate": gate, "up": up, "h": h, "h_bf16": h_bf16,

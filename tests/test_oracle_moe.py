@@ -114,6 +114,10 @@ def test_routed_bf16_equals_per_expert_baseline_loop():
     r = M.routed_bf16(x, ids, w, ex, n_experts=E)
     base = M.baseline_loop_bf16(x, ids, w, ex, n_experts=E)
     assert np.array_equal(r["y"], base)
+    # spreading the experts over threads (the CPU baseline does) changes nothing
+    rt = M.routed_bf16(x, ids, w, ex, n_experts=E, workers=4)
+    for k in ("gate", "up", "h_bf16", "out", "y"):
+        assert np.array_equal(rt[k], r[k]), k
 
 
 def test_routed_bf16_exactness_of_fp8_and_fp4_operands():
