@@ -35,6 +35,7 @@ HBM_PEAK_GBS = 8000.0
 MXFP4_PEAK_TFLOPS = 10100.0
 FP8_PEAK_TFLOPS = 5000.0
 BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
 D, I, E = 4096, 2048, 256
 EXPERT_BYTES = 2 * (I * D // 2 + I * D // 32) + (D * I // 2 + D * I // 32)  # 13,369,344
 GATEUP_BYTES = 2 * (I * D // 2 + I * D // 32)                                  # 8,912,896
@@ -49,7 +50,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default="",
-                    help="profile helper: run only 'decode', 'dequant', 'prefill' or 'offload'")
+                    help="profile helper: run only 'decode', 'dequant', 'prefill', 'router' or 'offload'")
     ap.add_argument("--offload-steps", type=int, default=512, help="decode steps of the expert-offload leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy 1 GiB device-to-device (a plain copy of known size for counter calibration)")
@@ -271,6 +272,34 @@ def measure_offload(dev, n_steps=512, n_layers=8, n_slots=512, T=8, K=8, warmup_
     return res
 
 
+def measure_router(dev, iters=200):
+    """dsv4_moe_route (gate logits + score + top-8 + weights) at decode and prefill
+    token counts: 256 experts, hidden 4096, fp32 gate weight, sqrt(softplus) scores
+    with a correction bias."""
+    from dsv4_hip import ops
+    rng = np.random.default_rng(31)
+    w = torch.from_numpy((rng.standard_normal((E, D)) * 0.03).astype(np.float32)).to(dev)
+    b = torch.from_numpy((rng.standard_normal(E) * 0.1).astype(np.float32)).to(dev)
+    res = {}
+    for Tn in (8, 2048):
+        x = torch.from_numpy(rng.standard_normal((Tn, D)).astype(np.float32)).to(torch.bfloat16).to(dev)
+        for _ in range(5):
+            ops.route(x, w, 8, "sqrtsoftplus", bias=b)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(iters):
+            ops.route(x, w, 8, "sqrtsoftplus", bias=b)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / iters
+        byts = E * D * 4 + Tn * D * 2 + Tn * 8 * 8
+        flops = 2.0 * Tn * E * D
+        res[f"tokens_{Tn}"] = {"us": us, "gbs": byts / us / 1e3, "tflops_fp32": flops / us / 1e6,
+                               "frac_fp32_mfma_peak": flops / us / 1e6 / FP32_PEAK_TFLOPS}
+    return res
+
+
 def cpu_baseline(sample_steps=2, threads=None, min_seconds=10.0):
     """numpy oracle of the same bf16 decode layer (8 tokens, top-8 of 256, hidden 4096,
     inter 2048) on the host cores: experts spread over min(host cores, 16) threads,
@@ -377,6 +406,8 @@ def main():
                            "frac_hbm": byts / s2 / 1e9 / HBM_PEAK_GBS, "active_experts": A}
         del pools, tables
         torch.cuda.empty_cache()
+    if not args.no_extra and args.only in ("", "router"):
+        extra["router"] = measure_router(dev)
     if not args.no_extra and args.only in ("", "offload") and args.offload_steps > 0:
         extra["offload_config4"] = measure_offload(dev, n_steps=args.offload_steps)
     if extra:

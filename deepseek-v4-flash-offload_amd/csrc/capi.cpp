@@ -169,6 +169,38 @@ int dsv4_moe_combine(const void* out_flat, const void* topk_ids, int ids_int64, 
 }
 
 // ---------------------------------------------------------------------------
+int64_t dsv4_moe_route_workspace_bytes(int T, int D, int E) {
+  if (T <= 0 || D <= 0 || E <= 0) return 0;
+  return (int64_t)route_split_k(T, D, E) * T * E * (int64_t)sizeof(float);
+}
+
+int dsv4_moe_route(const void* x, int x_f32, const float* gate_w, const float* bias, const void* tid2eid,
+                   int tid2eid_int64, int64_t vocab, const void* input_ids, int input_ids_int64, int T, int D, int E,
+                   int K, int scoring, int renormalize, float scale, float* out_w, int32_t* out_ids, int32_t* status,
+                   void* workspace, void* stream) {
+  REQUIRE(T >= 0, DSV4_ERR_SHAPE, "route: negative T");
+  REQUIRE(D > 0 && D % 32 == 0, DSV4_ERR_SHAPE, "route: hidden size %d not a positive multiple of 32", D);
+  REQUIRE(E >= 16 && E <= 512 && E % 16 == 0, DSV4_ERR_UNSUPPORTED,
+          "route: %d experts unsupported (multiple of 16 in 16..512)", E);
+  REQUIRE(K >= 1 && K <= E && K <= 64, DSV4_ERR_UNSUPPORTED, "route: top-k %d outside 1..min(E, 64)", K);
+  REQUIRE(scoring >= 0 && scoring <= 2, DSV4_ERR_UNSUPPORTED,
+          "route: scoring %d unknown (0 softmax, 1 sigmoid, 2 sqrtsoftplus)", scoring);
+  if (T == 0) return DSV4_OK;
+  REQUIRE(x && gate_w && out_w && out_ids && workspace, DSV4_ERR_NULL, "route: null pointer");
+  if (tid2eid) {
+    REQUIRE(input_ids, DSV4_ERR_NULL, "route: hash-layer routing needs input_ids");
+    REQUIRE(vocab > 0, DSV4_ERR_SHAPE, "route: tid2eid needs vocab > 0");
+  }
+  REQUIRE(aligned(x, 16) && aligned(gate_w, 16) && aligned(workspace, 4), DSV4_ERR_SHAPE,
+          "route: misaligned buffer (x and gate_w need 16 bytes)");
+  REQUIRE(x_f32 == 0 || x_f32 == 1, DSV4_ERR_UNSUPPORTED, "route: x_f32 must be 0 (bf16) or 1 (fp32)");
+  return hip_status(launch_moe_route(x, x_f32, gate_w, T, D, E, K, scoring, bias, tid2eid, tid2eid_int64,
+                                     input_ids, input_ids_int64, vocab, renormalize, scale, out_w, out_ids, status,
+                                     (float*)workspace, (hipStream_t)stream),
+                    "route launch");
+}
+
+// ---------------------------------------------------------------------------
 static int check_gemm_common(int afmt, const void* a, const void* a_scale, const int32_t* sorted_ids,
                              const int32_t* block_expert, const int32_t* npp, int R, int max_blocks,
                              const void* experts, int Kdim, void* out) {

@@ -88,3 +88,10 @@ hipError_t launch_moe_gemm_gateup(const Dsv4GemmArgs& a, hipStream_t st);
 hipError_t launch_moe_gemm_down(const Dsv4GemmArgs& a, hipStream_t st);
 bool moe_gemm_supported_kdim(int kdim);  // reduction lengths with a compiled kernel (512..8192, powers of two)
 bool moe_gemm_supported_block_m(int bm);  // 16 (decode kernel), 64 or 128 (tiled kernel)
+
+// Router: partial logits [S, T, E] in `part`, then scores / top-k / weights.
+int route_split_k(int T, int D, int E);
+hipError_t launch_moe_route(const void* x, int x_f32, const float* gate_w, int T, int D, int E, int K, int scoring,
+                            const float* bias, const void* tid2eid, int tid_is64, const void* input_ids,
+                            int ids_is64, int64_t vocab, int renorm, float scale, float* out_w,
+                            int32_t* out_ids, int32_t* status, float* part, hipStream_t st);

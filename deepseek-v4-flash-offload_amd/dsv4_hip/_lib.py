@@ -18,6 +18,7 @@ PROFILE_BF16 = 0
 PROFILE_A4W4 = 1
 RULE_CEIL_DIV6 = 0
 RULE_OCP_FLOOR = 1
+SCORING = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
 GEMM_BLOCK_M = 16
 MAX_EXPERTS = 512
 MAX_TOPK = 32
@@ -34,6 +35,9 @@ SIGNATURES = {
     "dsv4_mxfp4_dequant_bf16": (_i32, [_c_p, _c_p, _c_p, _i64, _i64, _c_p]),
     "dsv4_fp8_act_quant": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "dsv4_mxfp4_act_quant": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p]),
+    "dsv4_moe_route_workspace_bytes": (_i64, [_i32, _i32, _i32]),
+    "dsv4_moe_route": (_i32, [_c_p, _i32, _c_p, _c_p, _c_p, _i32, _i64, _c_p, _i32, _i32, _i32, _i32, _i32, _i32,
+                              _i32, _f32, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "dsv4_moe_align_max_blocks": (_i32, [_i32, _i32, _i32]),
     "dsv4_moe_align": (_i32, [_c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32] + [_c_p] * 13 + [_c_p]),
     "dsv4_moe_permute": (_i32, [_c_p, _i64, _c_p, _i64, _i64, _c_p, _c_p]),

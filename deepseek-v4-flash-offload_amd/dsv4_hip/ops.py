@@ -143,6 +143,54 @@ class AlignResult:
         return self.active[: int(self.num_active.item())]
 
 
+def route(x: torch.Tensor, gate_w: torch.Tensor, topk: int, scoring: str = "sqrtsoftplus",
+          bias: Optional[torch.Tensor] = None, renormalize: bool = True, scale: float = 1.5,
+          tid2eid: Optional[torch.Tensor] = None, input_ids: Optional[torch.Tensor] = None,
+          status: Optional[torch.Tensor] = None):
+    """Router of ``deepseek_v4.py:118-148`` on the device: ``(weights fp32 [T, K],
+    ids int32 [T, K])``. ``x`` [T, D] bf16 or fp32 (other dtypes are cast to fp32,
+    as ``hs.float()`` does), ``gate_w`` [E, D] fp32;
+    ``bias`` [E] fp32 or None; ``tid2eid`` [vocab, K] int32/int64 with
+    ``input_ids`` [T] on hash layers. ``status`` (int32 [1], optional) is
+    incremented once per out-of-range input id or table entry."""
+    _dev(x, "route")
+    if scoring not in _lib.SCORING:
+        raise ValueError(f"route: unknown scoring function {scoring!r}")
+    x = x.reshape(-1, x.shape[-1])
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        x = x.float()
+    x = x.contiguous()
+    T, D = x.shape
+    w = gate_w.to(torch.float32).contiguous()
+    if w.dim() != 2 or w.shape[1] != D:
+        raise ValueError(f"route: gate weight {tuple(w.shape)} does not match hidden size {D}")
+    E = w.shape[0]
+    b = None if bias is None else bias.to(torch.float32).contiguous()
+    tab, ids_in, vocab = None, None, 0
+    if tid2eid is not None:
+        if input_ids is None:
+            raise RuntimeError("hash-layer routing needs input_ids")
+        tab = tid2eid.contiguous()
+        if tab.dtype not in (torch.int32, torch.int64) or tab.dim() != 2 or tab.shape[1] != topk:
+            raise ValueError("route: tid2eid must be int32/int64 [vocab, topk]")
+        ids_in = input_ids.reshape(-1).contiguous()
+        if ids_in.dtype not in (torch.int32, torch.int64):
+            ids_in = ids_in.to(torch.int64)
+        if ids_in.numel() != T:
+            raise ValueError(f"route: {ids_in.numel()} input ids for {T} tokens")
+        vocab = tab.shape[0]
+    dev = x.device
+    out_w = torch.empty(T, topk, dtype=torch.float32, device=dev)
+    out_ids = torch.empty(T, topk, dtype=torch.int32, device=dev)
+    ws = torch.empty(max(int(_lib.lib().dsv4_moe_route_workspace_bytes(T, D, E)), 4), dtype=torch.uint8,
+                     device=dev)
+    call("dsv4_moe_route", _p(x), 1 if x.dtype == torch.float32 else 0, _p(w), _p(b), _p(tab), 1 if tab is not None and tab.dtype == torch.int64 else 0,
+         vocab, _p(ids_in), 1 if ids_in is not None and ids_in.dtype == torch.int64 else 0, T, D, E, topk,
+         _lib.SCORING[scoring], 1 if renormalize else 0, float(scale), _p(out_w), _p(out_ids), _p(status), _p(ws),
+         _stream(x))
+    return out_w, out_ids
+
+
 def max_blocks(R: int, E: int, block_m: int) -> int:
     return int(_lib.lib().dsv4_moe_align_max_blocks(R, E, block_m))
 

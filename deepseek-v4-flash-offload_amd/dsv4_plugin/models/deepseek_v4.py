@@ -7,8 +7,8 @@ is_draft_layer=False)`` with ``_route`` / ``_routed`` / ``_routed_mxfp4`` /
 ``DSV4_MXFP4_GMM``), ``_offload_load_weights``, ``_ORIG_LOAD_WEIGHTS`` and
 ``install_patches``.
 
-Routing (``_route``) keeps the reference's torch math on the device. The
-routed experts run as ONE call into ``libdsv4hip.so``
+Routing (``_route``) runs the HIP router (``dsv4_moe_route``) on device
+tensors. The routed experts run as ONE call into ``libdsv4hip.so``
 (``dsv4_moe_layer_forward``): moe_align, activation quantisation, the grouped
 gate/up GEMM with the SwiGLU epilogue, the h quantisation, the grouped down
 GEMM and the deterministic combine. Expert weights are read in place from the
@@ -141,10 +141,21 @@ class OffloadDeepseekV4MoE(_BASE):
         self.engine = get_engine()
         self.experts = _ExpertsFacade(self)
 
-    # -- routing (reference math, torch on the device) -----------------------
+    # -- routing ---------------------------------------------------------------
     def _route(self, hs: torch.Tensor, input_ids):
         """``noaux_tc`` + score function routing: biased scores choose, unbiased
-        scores weigh, renormalise, scale (``deepseek_v4.py:118-148``)."""
+        scores weigh, renormalise, scale (``deepseek_v4.py:118-148``).
+
+        Device tensors go through the HIP router (``dsv4_moe_route``: ids int32,
+        each token's picks in descending biased score). Host tensors use the
+        same math in torch, as the reference writes it."""
+        if self.hash and input_ids is None:
+            raise RuntimeError("hash-layer routing needs input_ids (forward_context.input_ids is missing)")
+        if hs.is_cuda:
+            return _ops.route(hs, self.gate.weight, self.topk, self.scoring_func,
+                              bias=None if self.hash else self.gate.e_score_correction_bias,
+                              renormalize=bool(self.renormalize), scale=float(self.routed_scaling_factor),
+                              tid2eid=self.gate.tid2eid if self.hash else None, input_ids=input_ids)
         gating = F.linear(hs.float(), self.gate.weight)
         if self.scoring_func == "softmax":
             scores = gating.softmax(dim=-1)
@@ -153,8 +164,6 @@ class OffloadDeepseekV4MoE(_BASE):
         else:  # sqrtsoftplus
             scores = F.softplus(gating).sqrt()
         if self.hash:
-            if input_ids is None:
-                raise RuntimeError("hash-layer routing needs input_ids (forward_context.input_ids is missing)")
             indices = self.gate.tid2eid[input_ids.to(torch.long).flatten()]
         else:
             bias = self.gate.e_score_correction_bias

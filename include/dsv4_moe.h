@@ -82,6 +82,26 @@ int dsv4_fp8_act_quant(const void* x, int64_t rows, int64_t cols, int block_size
 int dsv4_mxfp4_act_quant(const void* x, int64_t rows, int64_t cols, int rule, void* packed, void* scale, void* dq,
                          void* stream);
 
+/* Router of one MoE layer, OffloadDeepseekV4MoE._route (deepseek_v4.py:118-148):
+ *   logits = float(x) @ gate_wᵀ (fp32), scores = softmax (scoring 0) | sigmoid (1)
+ *   | sqrt(softplus) (2, threshold 20 as F.softplus); ids = top-K of scores + bias
+ *   (bias NULL: none), or on hash layers (tid2eid non-NULL) ids[t] =
+ *   tid2eid[input_ids[t]] with tid2eid [vocab, K] int32/int64; out_w = scores[ids],
+ *   divided by their sum when renormalize, times scale (routed_scaling_factor).
+ * x [T, D] bf16 (x_f32 = 0) or fp32 (1); gate_w fp32 [E, D]; out_w fp32 [T, K]; out_ids int32 [T, K], each
+ * token's ids in descending biased score with ties to the lower id (the reference's
+ * topk(sorted=False) leaves order and tie rule open), or in table order on hash
+ * layers. status [1] (nullable, zeroed by the caller) is incremented once per input
+ * id outside [0, vocab) and per table entry outside [0, E); such picks get id -1
+ * and weight 0.
+ * Limits: D % 32 == 0, E % 16 == 0, 16 <= E <= 512, 1 <= K <= min(E, 64).
+ * workspace: dsv4_moe_route_workspace_bytes(T, D, E) bytes (partial logits). */
+int64_t dsv4_moe_route_workspace_bytes(int T, int D, int E);
+int dsv4_moe_route(const void* x, int x_f32, const float* gate_w, const float* bias, const void* tid2eid,
+                   int tid2eid_int64, int64_t vocab, const void* input_ids, int input_ids_int64, int T, int D, int E,
+                   int K, int scoring, int renormalize, float scale, float* out_w, int32_t* out_ids, int32_t* status,
+                   void* workspace, void* stream);
+
 /* Upper bound of padded M blocks for R routed entries (host function). */
 int dsv4_moe_align_max_blocks(int R, int E, int block_m);
 

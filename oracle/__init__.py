@@ -14,8 +14,9 @@ Modules and the reference code each one follows:
   the OCP-MX ``floor(log2 amax) - 2`` activation rule that stands in for the
   closed ``npu_dynamic_mx_quant`` (``deepseek_v4.py:212,240``).
 * ``routing`` - ``deepseek_v4.py:150-164`` sort/count/active (moe_align) with
-  the stable order, the row gather of ``:171,213-214`` and the unweighted
-  ``index_add_`` unpermute of ``:195-197``.
+  the stable order, the row gather of ``:171,213-214``, the unweighted
+  ``index_add_`` unpermute of ``:195-197`` and the router ``_route`` of
+  ``:118-148``.
 * ``moe``     - ``deepseek_v4.py:166-245`` (bf16 profile and a4w4 profile of
   ``_routed``), ``model_npu.py:492-533`` (per-expert loop baseline).
 * ``lru``     - ``offload.py:86-129`` (OrderedDict LRU and its counters).

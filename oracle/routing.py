@@ -11,6 +11,12 @@ Follows ``dsv4_plugin/models/deepseek_v4.py`` of the reference:
 * ``permute``    - ``x_sorted = xq[row]``, ``:171`` / ``:213-214``.
 * ``unpermute``  - ``y = zeros(fp32); y.index_add_(0, row, out.float());
   y.to(bf16)``, ``:195-197`` / ``:243-245`` (unweighted, fp32, in sorted order).
+* ``route``      - ``OffloadDeepseekV4MoE._route``, ``:118-148``: fp32 gate
+  logits, softmax / sigmoid / sqrt(softplus) scores, top-k of the biased scores
+  (or the ``tid2eid`` row of each token on hash layers), the unbiased scores of
+  the chosen experts as weights, renormalised and scaled. Computed in float64;
+  ties in the top-k go to the lower expert id (``topk(sorted=False)`` leaves
+  both the tie rule and the output order open).
 """
 
 import numpy as np
@@ -81,3 +87,41 @@ def unpermute(out_sorted_bf16, row, T):
     y = np.zeros((T, D), dtype=np.float32)
     np.add.at(y, np.asarray(row), out)
     return f32_to_bf16_bits(y)
+
+
+def _softplus(l):
+    """``F.softplus`` (beta 1, threshold 20): ``l`` above the threshold, else
+    ``log1p(exp(l))``."""
+    with np.errstate(over="ignore"):
+        return np.where(l > 20.0, l, np.log1p(np.exp(np.minimum(l, 20.0))))
+
+
+def route(x_bf16, gate_w, topk, scoring="sqrtsoftplus", bias=None, renormalize=True,
+          scale=1.5, tid2eid=None, input_ids=None):
+    """``deepseek_v4.py:118-148`` in float64.
+
+    ``x_bf16`` [T, D] bf16 bit patterns, ``gate_w`` [E, D] fp32. Returns
+    ``(weights [T, K] float64, ids [T, K] int64, scores [T, E] float64)`` with the
+    ids of a token in descending order of the biased score."""
+    x = bf16_bits_to_f32(np.asarray(x_bf16, np.uint16)).astype(np.float64)
+    logits = x @ np.asarray(gate_w, np.float32).astype(np.float64).T          # :125
+    if scoring == "softmax":                                                  # :126-131
+        e = np.exp(logits - logits.max(axis=-1, keepdims=True))
+        scores = e / e.sum(axis=-1, keepdims=True)
+    elif scoring == "sigmoid":
+        scores = 1.0 / (1.0 + np.exp(-logits))
+    elif scoring == "sqrtsoftplus":
+        scores = np.sqrt(_softplus(logits))
+    else:
+        raise ValueError(f"unknown scoring function {scoring!r}")
+    if tid2eid is not None:                                                   # :133-138
+        if input_ids is None:
+            raise RuntimeError("hash-layer routing needs input_ids")
+        ids = np.asarray(tid2eid)[np.asarray(input_ids).astype(np.int64).reshape(-1)].astype(np.int64)
+    else:                                                                     # :139-142
+        choice = scores if bias is None else scores + np.asarray(bias, np.float32).astype(np.float64)
+        ids = np.argsort(-choice, axis=-1, kind="stable")[:, :topk].astype(np.int64)
+    w = np.take_along_axis(scores, ids, axis=1)                               # :144
+    if renormalize:                                                           # :145-146
+        w = w / w.sum(axis=-1, keepdims=True)
+    return w * scale, ids, scores                                             # :147

@@ -97,3 +97,33 @@ def test_ops_reject_cpu_tensors():
         ops.dequant_mxfp4(torch.zeros(4, 16, dtype=torch.uint8), torch.zeros(4, 1, dtype=torch.uint8))
     with pytest.raises(RuntimeError, match="ROCm device"):
         ops.moe_align(torch.zeros(4, 2, dtype=torch.int64), None, 8)
+
+
+def test_route_validation():
+    lib = _lib.lib()
+    args = dict(x=None, x_f32=0, w=None, bias=None, tab=None, tab64=0, vocab=0, ids=None, ids64=0, T=4, D=4096,
+                E=256, K=8, scoring=2, renorm=1, scale=1.5, ow=None, oi=None, st=None, ws=None, stream=None)
+
+    def route(**kw):
+        a = dict(args, **kw)
+        return _err(lib.dsv4_moe_route(*a.values()))
+
+    rc, msg = route(D=4080)
+    assert rc == -2 and "multiple of 32" in msg
+    rc, msg = route(E=250)
+    assert rc == -3 and "experts" in msg
+    rc, msg = route(E=1024)
+    assert rc == -3
+    rc, msg = route(K=0)
+    assert rc == -3 and "top-k" in msg
+    rc, msg = route(K=65, E=512)
+    assert rc == -3
+    rc, msg = route(scoring=3)
+    assert rc == -3 and "scoring" in msg
+    rc, msg = route()
+    assert rc == -1 and "null" in msg
+    assert route(T=0)[0] == 0  # no tokens is a no-op
+    # the partial-logit workspace [S, T, E]: K split 16 ways at decode sizes, 4 ways at 2048 tokens
+    assert lib.dsv4_moe_route_workspace_bytes(8, 4096, 256) == 16 * 8 * 256 * 4
+    assert lib.dsv4_moe_route_workspace_bytes(2048, 4096, 256) == 4 * 2048 * 256 * 4
+    assert lib.dsv4_moe_route_workspace_bytes(0, 4096, 256) == 0
