@@ -318,7 +318,12 @@ static int slots_fetch(dsv4_slots* s, int layer, const int32_t* eids, int n, hip
     int rc = release_locked(s, compute);
     if (rc) return rc;
   }
-  const uint32_t mark = ++s->batch_mark == 0 ? ++s->batch_mark : s->batch_mark;
+  // An acquire starts a new batch. A prefetch joins the current one: the slots
+  // the last acquire handed out are still to be read by work the caller has not
+  // enqueued yet (their release is recorded only at the next acquire), so they
+  // must not become a prefetch's victims.
+  const uint32_t mark =
+      is_acquire ? (++s->batch_mark == 0 ? ++s->batch_mark : s->batch_mark) : s->batch_mark;
   int64_t wait_seq = 0;
   bool issued = false;
   int misses = 0;
@@ -334,6 +339,7 @@ static int slots_fetch(dsv4_slots* s, int layer, const int32_t* eids, int n, hip
       if (s->lru.lookup(key, &tmp)) continue;  // already resident or in flight: leave recency alone
     }
     const int r = s->lru.access(key, mark, &slot, &evicted);
+    if (r < 0 && !is_acquire) break;  // a prefetch is advisory: stop when only pinned slots are left
     SREQ(r >= 0, DSV4_ERR_STATE, "slots: all %d slots are pinned by this batch", s->n_slots);
     if (r == 1) {
       if (is_acquire) ++s->hits;

@@ -23,6 +23,7 @@ otherwise the class is a plain ``nn.Module`` (shared experts omitted) and
 
 import importlib
 import os
+import weakref
 
 import numpy as np
 import torch
@@ -52,6 +53,14 @@ _MXFP4_GMM = os.environ.get("DSV4_MXFP4_GMM", "0") == "1"
 # activation scale rule of the a4w4 profile: "ocp_floor" or "ceil_div6"
 _MX_RULE = os.environ.get("DSV4_MX_RULE", "ocp_floor")
 _RULES = {"ocp_floor": _lib.RULE_OCP_FLOOR, "ceil_div6": _lib.RULE_CEIL_DIV6}
+
+# Predictive prefetch: layer L routes its input with layer L+1's gate (or reads
+# layer L+1's tid2eid rows on hash layers, which is exact) and starts the copies
+# of the experts that picks, after its own slots are acquired and before its
+# GEMMs, so the copies overlap its compute. Read at call time; env
+# DSV4_PREFETCH_NEXT=1. Layers register themselves by index.
+_PREFETCH_NEXT = os.environ.get("DSV4_PREFETCH_NEXT", "0") == "1"
+_LAYERS = weakref.WeakValueDictionary()
 
 _BASE = v4.DeepseekV4MoE if (v4 is not None and hasattr(v4, "DeepseekV4MoE")) else nn.Module
 _RUNNERS = {}
@@ -140,6 +149,7 @@ class OffloadDeepseekV4MoE(_BASE):
                 torch.zeros(config.n_routed_experts, dtype=torch.float32))
         self.engine = get_engine()
         self.experts = _ExpertsFacade(self)
+        _LAYERS[self.layer_idx] = self
 
     # -- routing ---------------------------------------------------------------
     def _route(self, hs: torch.Tensor, input_ids):
@@ -189,12 +199,31 @@ class OffloadDeepseekV4MoE(_BASE):
         inter = next(iter(packed.values()))["w1p"].shape[0]
         return _ops.expert_table(packed, E, device), inter
 
-    def _run_experts(self, hs, weights, indices, profile):
+    def _prefetch_next(self, hs, input_ids):
+        """Start the copies of the experts layer ``layer_idx + 1`` is predicted to
+        use; returns the number of copies started."""
+        nxt = _LAYERS.get(self.layer_idx + 1)
+        eng = self.engine
+        if nxt is None or not hasattr(eng, "prefetch") or nxt.engine is not eng:
+            return 0
+        if nxt.hash:
+            if input_ids is None:
+                return 0
+            ids = nxt.gate.tid2eid[input_ids.to(torch.long).flatten()]
+        else:
+            _, ids = nxt._route(hs, None)
+        ids = ids.detach().to("cpu").numpy().reshape(-1)
+        ids = np.unique(ids[(ids >= 0) & (ids < nxt.n_routed_experts)])
+        return eng.prefetch(nxt.layer_idx, ids) if ids.size else 0
+
+    def _run_experts(self, hs, weights, indices, profile, input_ids=None):
         T, D = hs.shape
         x = hs if (hs.dtype == torch.bfloat16 and hs.is_contiguous()) else hs.to(torch.bfloat16).contiguous()
         if T == 0:
             return torch.zeros_like(hs)
         table, inter = self._expert_table(indices, hs.device)
+        if _PREFETCH_NEXT:
+            self._prefetch_next(hs, input_ids)
         limit = self.swiglu_limit if (self.swiglu_limit and self.swiglu_limit > 0) else 0.0
         y = _runner(hs.device, self.n_routed_experts, D, inter).forward(
             x, indices, weights, table, profile=profile, rule=_RULES[_MX_RULE], swiglu_limit=limit)
@@ -205,7 +234,7 @@ class OffloadDeepseekV4MoE(_BASE):
         profile when the module toggle ``_MXFP4_GMM`` is set (``:199-245``)."""
         weights, indices = self._route(hs, input_ids)
         profile = _lib.PROFILE_A4W4 if _MXFP4_GMM else _lib.PROFILE_BF16
-        return self._run_experts(hs, weights, indices, profile)
+        return self._run_experts(hs, weights, indices, profile, input_ids)
 
     def _routed_mxfp4(self, s_w, row, active, group_list, T, hs):
         """a4w4 path from the reference's sorted view (``deepseek_v4.py:199``

@@ -211,7 +211,10 @@ int dsv4_slots_num_registered(dsv4_slots* s, int64_t* n);
  * readers are the work enqueued on compute_stream before this call). */
 int dsv4_slots_acquire(dsv4_slots* s, int layer, const int32_t* eids, int n, void* compute_stream,
                        int32_t* slots, int* n_miss);
-/* Starts copies for the non-resident experts of a later batch (no waits). */
+/* Starts copies for the non-resident experts of a later batch (no waits) and
+ * sets *n_issued to the number started. The slots the last acquire returned
+ * are never evicted for it (their readers may not be enqueued yet); when only
+ * those are left the prefetch stops early. */
 int dsv4_slots_prefetch(dsv4_slots* s, int layer, const int32_t* eids, int n, int* n_issued);
 int dsv4_slots_release(dsv4_slots* s, void* compute_stream);
 int dsv4_slots_copy_record(dsv4_slots* s, int layer, int eid, void* dst, void* stream);

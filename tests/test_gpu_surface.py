@@ -328,3 +328,50 @@ def test_slot_cache_matches_lru_oracle_under_drifting_zipf(gpu):
     assert (st["hits"], st["misses"], st["evictions"]) == (so["hits"], so["misses"], so["evictions"])
     assert so["evictions"] > 100 and st["bytes_h2d"] == st["misses"] * layout.record_bytes
     cache.close()
+
+
+@pytest.mark.parametrize("n_slots,next_hash", [(64, False), (64, True), (20, False)])
+def test_prefetch_next_layer(gpu, monkeypatch, n_slots, next_hash):
+    # Layer 3 predicts layer 4's experts (layer 4's gate on layer 3's input, or
+    # layer 4's tid2eid rows) and starts their copies before its own GEMMs. With
+    # room for both layers the prediction (exact here: layer 4 runs on the same
+    # input) leaves layer 4 no misses; with 20 slots the prefetch may not evict
+    # the slots layer 3 is about to read, and both layers stay exact.
+    E, K, D, I, T = 32, 4, 1024, 512, 4
+    monkeypatch.setenv("DSV4_PACKED_SLOTS", str(n_slots))
+    engine = ExpertOffloadEngine(slot_capacity=4, device="cuda:0")
+    host = {}
+    for layer in (3, 4):
+        for e in range(E):
+            host[layer, e] = synth.expert_weights(100 * layer + e, D, I)
+            for w in ("w1", "w2", "w3"):
+                engine.capture(f"layers.{layer}.ffn.experts.{e}.{w}.weight",
+                               torch.from_numpy(host[layer, e][w + "p"]).view(torch.int8))
+                engine.capture(f"layers.{layer}.ffn.experts.{e}.{w}.scale",
+                               torch.from_numpy(host[layer, e][w + "s"]).view(torch.float8_e8m0fnu))
+    m3 = _make_plugin(engine, E, K, 3, False, D)
+    m4 = _make_plugin(engine, E, K, 4, next_hash, D)
+    monkeypatch.setitem(mod._LAYERS, 3, m3)
+    monkeypatch.setitem(mod._LAYERS, 4, m4)
+    monkeypatch.setattr(mod, "_PREFETCH_NEXT", True)
+    x = (synth.bf16_normal(np.random.default_rng(6), (T, D)).float() * 0.5).to(torch.bfloat16).to(gpu)
+    ids = torch.randint(0, 100, (T,), generator=torch.Generator().manual_seed(3)).to(gpu)
+    y3 = m3._routed(x, ids)
+    s3 = engine.stats()
+    _, idx4 = m4._route(x, ids)
+    want4 = len(np.unique(idx4.cpu().numpy()))
+    assert s3["prefetched"] > 0
+    if n_slots == 64:
+        assert s3["prefetched"] == want4
+    y4 = m4._routed(x, ids)
+    torch.cuda.synchronize()
+    s4 = engine.stats()
+    if n_slots == 64:
+        assert s4["packed_misses"] == s3["packed_misses"]   # every layer-4 expert was prefetched
+        assert s4["packed_hits"] - s3["packed_hits"] == want4
+    xb = _bits(x)
+    for m, y, layer in ((m3, y3, 3), (m4, y4, 4)):
+        w, idx = m._route(x, ids)
+        ref = M.routed_bf16(xb, idx.cpu().numpy(), w.cpu().numpy(), {e: host[layer, e] for e in range(E)},
+                            n_experts=E)
+        assert rel(Q.bf16_bits_to_f32(_bits(y)), Q.bf16_bits_to_f32(ref["y"])) <= 1e-2, layer
