@@ -48,9 +48,12 @@ __device__ int block_exclusive_scan(int v, int* lds_waves, int* out_total) {
   return r;
 }
 
+// n_shared > 0 appends the shared expert as one more group after the routed
+// experts: n_shared rows with flat indices R .. R+n_shared-1, block_expert = E.
+// The padding sentinel is then R + n_shared.
 template <typename IdT, int NT>
 __device__ void align_body(const IdT* __restrict__ ids, const float* __restrict__ topk_w, int R, int K, int E,
-                           int block_m, int max_blocks, const Dsv4AlignOut& o) {
+                           int block_m, int max_blocks, const Dsv4AlignOut& o, int n_shared = 0) {
   constexpr int kThreads = NT;
   constexpr int kWaves = NT / 64;
   extern __shared__ int lds[];
@@ -91,16 +94,28 @@ __device__ void align_body(const IdT* __restrict__ ids, const float* __restrict_
     if (o.active) o.active[tid] = -1;
   }
   __syncthreads();
-  const int total_blocks = totals[1] / block_m;
+  const int pad_id = R + n_shared;  // padding sentinel
+  const int shared_padded = ((n_shared + block_m - 1) / block_m) * block_m;
+  const int total_padded = totals[1] + shared_padded;
+  const int total_blocks = total_padded / block_m;
+  const int cap = max_blocks * block_m;
   if (tid < E) {
     if (o.active && c > 0) o.active[oa] = tid;
     const int b0 = op / block_m, b1 = min((op + padded) / block_m, max_blocks);
     for (int b = b0; b < b1; ++b) o.block_expert[b] = tid;
-    const int p1 = min(op + padded, max_blocks * block_m);
-    for (int p = op + c; p < p1; ++p) o.sorted_ids[p] = R;  // padding sentinel
+    const int p1 = min(op + padded, cap);
+    for (int p = op + c; p < p1; ++p) o.sorted_ids[p] = pad_id;
+  }
+  // the shared expert's group: rows R + i in order, after every routed expert
+  for (int i = tid; i < shared_padded; i += kThreads) {
+    const int p = totals[1] + i;
+    if (p < cap) {
+      o.sorted_ids[p] = i < n_shared ? R + i : pad_id;
+      if (i % block_m == 0) o.block_expert[p / block_m] = E;
+    }
   }
   if (tid == 0) {
-    o.num_post_padded[0] = min(totals[1], max_blocks * block_m);
+    o.num_post_padded[0] = min(total_padded, cap);
     if (o.num_active) o.num_active[0] = totals[2];
     if (o.status) o.status[0] = bad + (total_blocks > max_blocks ? (1 << 30) : 0);
   }
@@ -167,9 +182,9 @@ __global__ __launch_bounds__(NT) void moe_align_quant_kernel(const IdT* __restri
                                                              int E, int block_m, int max_blocks,
                                                              Dsv4AlignOut o, const uint4* __restrict__ x,
                                                              int64_t n_groups, int rule, void* q_codes,
-                                                             void* q_scale) {
+                                                             void* q_scale, int n_shared) {
   if (blockIdx.x == 0) {
-    align_body<IdT, NT>(ids, topk_w, R, K, E, block_m, max_blocks, o);
+    align_body<IdT, NT>(ids, topk_w, R, K, E, block_m, max_blocks, o, n_shared);
     return;
   }
   const int64_t g = (int64_t)(blockIdx.x - 1) * NT + threadIdx.x;
@@ -209,7 +224,7 @@ hipError_t launch_moe_align(const void* topk_ids, int ids_int64, const float* to
 hipError_t launch_moe_align_quant(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K, int E,
                                   int block_m, int max_blocks, const Dsv4AlignOut& o, const uint16_t* x,
                                   int64_t n_elems, int qfmt, int rule, void* q_codes, void* q_scale,
-                                  hipStream_t st) {
+                                  hipStream_t st, int n_shared) {
   const bool small = E <= 256 && R <= 2048;
   const int nt = small ? 256 : 1024;
   const size_t lds = sizeof(int) * (size_t)((E + 1) + E + E + (E + 1) + (nt / 64) * (E + 1));
@@ -219,7 +234,8 @@ hipError_t launch_moe_align_quant(const void* topk_ids, int ids_int64, const flo
   const dim3 grid((unsigned)(1 + qwg));
 #define DSV4_AQ(IDT, NT_, QF)                                                                              \
   hipLaunchKernelGGL((moe_align_quant_kernel<IDT, NT_, QF>), grid, dim3(NT_), lds, st, (const IDT*)topk_ids, \
-                     topk_w, R, K, E, block_m, max_blocks, o, (const uint4*)x, n_groups, rule, q_codes, q_scale)
+                     topk_w, R, K, E, block_m, max_blocks, o, (const uint4*)x, n_groups, rule, q_codes, q_scale, \
+                     n_shared)
   if (small) {
     if (ids_int64) { if (qfmt == 0) DSV4_AQ(long long, 256, 0); else DSV4_AQ(long long, 256, 1); }
     else { if (qfmt == 0) DSV4_AQ(int32_t, 256, 0); else DSV4_AQ(int32_t, 256, 1); }

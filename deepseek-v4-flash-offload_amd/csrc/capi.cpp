@@ -271,12 +271,13 @@ struct LayerWs {
 // from there on, where the Zipf-hot experts receive hundreds of rows.
 static int layer_block_m(int64_t R) { return R >= 2048 ? 64 : DSV4_GEMM_BLOCK_M; }
 
-static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile) {
+static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool shared = false) {
   LayerWs w{};
   const int64_t R = (int64_t)T * K;
+  const int64_t Rt = R + (shared ? T : 0);  // routed rows, then the shared expert's T rows
   const int bm = layer_block_m(R);
   w.bm = bm;
-  w.max_blocks = dsv4_moe_align_max_blocks((int)R, E, bm);
+  w.max_blocks = dsv4_moe_align_max_blocks((int)R, E, bm) + (shared ? (T + bm - 1) / bm : 0);
   const bool fp8 = profile == DSV4_PROFILE_BF16;
   int64_t o = 0;
   auto take = [&](int64_t bytes) { int64_t at = o; o = round_up(o + bytes, 256); return at; };
@@ -286,26 +287,20 @@ static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile) {
   w.status = take(sizeof(int32_t));
   w.xa = take(fp8 ? (int64_t)T * D : (int64_t)T * D / 2);
   w.xs = take((int64_t)T * D / 32);
-  w.h = take(2 * R * I);
-  w.ha = take(fp8 ? R * I : R * I / 2);
-  w.hs = take(R * I / 32);
-  w.out = take(2 * R * D);
+  w.h = take(2 * Rt * I);
+  w.ha = take(fp8 ? Rt * I : Rt * I / 2);
+  w.hs = take(Rt * I / 32);
+  w.out = take(2 * Rt * D);
   w.total = o;
   return w;
 }
 
-int dsv4_moe_layer_workspace_bytes(int T, int K, int E, int D, int I, int profile, int64_t* bytes) {
-  REQUIRE(bytes, DSV4_ERR_NULL, "workspace: null output");
-  REQUIRE(T >= 0 && K > 0 && E > 0 && D > 0 && I > 0, DSV4_ERR_SHAPE, "workspace: bad sizes");
-  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4, DSV4_ERR_UNSUPPORTED,
-          "workspace: unknown profile %d", profile);
-  *bytes = layer_ws(T, K, E, D, I, profile).total;
-  return DSV4_OK;
-}
-
-int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
-                           const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
-                           float swiglu_limit, void* workspace, int64_t workspace_bytes, void* y, void* stream) {
+// The routed layer, and with `shared` the shared expert as one more group of
+// T rows (bf16 profile only; checked by the caller).
+static int layer_forward(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
+                         const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
+                         const Dsv4ExpertPtrs* shared, float swiglu_limit, void* workspace, int64_t workspace_bytes,
+                         void* y, void* stream) {
   REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4, DSV4_ERR_UNSUPPORTED,
           "layer: unknown profile %d", profile);
   REQUIRE(T >= 0 && K > 0 && K <= DSV4_MAX_TOPK, DSV4_ERR_SHAPE, "layer: bad T=%d K=%d", T, K);
@@ -313,7 +308,7 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
           "layer: D=%d and I=%d must be multiples of 512", D, I);
   if (T == 0) return DSV4_OK;
   REQUIRE(x && topk_ids && topk_w && expert_table && workspace && y, DSV4_ERR_NULL, "layer: null pointer");
-  const LayerWs w = layer_ws(T, K, E, D, I, profile);
+  const LayerWs w = layer_ws(T, K, E, D, I, profile, shared != nullptr);
   REQUIRE(workspace_bytes >= w.total, DSV4_ERR_SHAPE, "layer: workspace %lld < %lld bytes",
           (long long)workspace_bytes, (long long)w.total);
   REQUIRE(aligned(workspace, 256), DSV4_ERR_SHAPE, "layer: workspace not 256-byte aligned");
@@ -323,6 +318,8 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
   int32_t* npp = (int32_t*)(base + w.npp);
   int32_t* status = (int32_t*)(base + w.status);
   const int R = T * K;
+  const int n_sh = shared ? T : 0;
+  const int Rt = R + n_sh;
   const int bm = w.bm;
   REQUIRE(E > 0 && E <= DSV4_MAX_EXPERTS, DSV4_ERR_UNSUPPORTED, "layer: E=%d outside 1..%d", E, DSV4_MAX_EXPERTS);
   REQUIRE(scale_rule == DSV4_RULE_CEIL_DIV6 || scale_rule == DSV4_RULE_OCP_FLOOR || profile == DSV4_PROFILE_BF16,
@@ -330,16 +327,16 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
   REQUIRE(aligned(x, 16), DSV4_ERR_SHAPE, "layer: x not 16-byte aligned");
   const bool fp8 = profile == DSV4_PROFILE_BF16;
   const int afmt = fp8 ? DSV4_AFMT_E4M3 : DSV4_AFMT_E2M1;
+  REQUIRE(moe_gemm_supported_kdim(D) && moe_gemm_supported_kdim(I), DSV4_ERR_UNSUPPORTED,
+          "layer: no GEMM compiled for D=%d / I=%d", D, I);
   // routing layout and the activation quantisation of x share one launch
   Dsv4AlignOut ao{sorted_ids, block_expert, npp, nullptr, nullptr, nullptr, nullptr, nullptr,
                   nullptr,    nullptr,      nullptr, nullptr, status};
   int rc = hip_status(launch_moe_align_quant(topk_ids, ids_int64, nullptr, R, K, E, bm, w.max_blocks, ao,
                                              (const uint16_t*)x, (int64_t)T * D, fp8 ? 0 : 1, scale_rule,
-                                             base + w.xa, base + w.xs, (hipStream_t)stream),
+                                             base + w.xa, base + w.xs, (hipStream_t)stream, n_sh),
                       "align+quant launch");
   if (rc) return rc;
-  REQUIRE(moe_gemm_supported_kdim(D) && moe_gemm_supported_kdim(I), DSV4_ERR_UNSUPPORTED,
-          "layer: no GEMM compiled for D=%d / I=%d", D, I);
   const Dsv4ExpertPtrs* table = (const Dsv4ExpertPtrs*)expert_table;
   // gate/up + SwiGLU, quantising h in the epilogue where the kernel holds whole blocks
   const bool hq_fused = !fp8 || bm != DSV4_GEMM_BLOCK_M;
@@ -352,7 +349,7 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
   gu.sorted_ids = sorted_ids;
   gu.block_expert = block_expert;
   gu.num_post_padded = npp;
-  gu.R = R;
+  gu.R = Rt;
   gu.block_m = bm;
   gu.max_blocks = w.max_blocks;
   gu.experts = table;
@@ -368,10 +365,16 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
     gu.hq_codes = (uint8_t*)(base + w.ha);
     gu.hq_scale = (uint8_t*)(base + w.hs);
   }
+  if (shared) {  // rows R.. read x row f - R with routing weight 1
+    gu.has_shared = 1;
+    gu.shared_expert = E;
+    gu.shared_a_rows = n_sh;
+    gu.shared = *shared;
+  }
   rc = hip_status(launch_moe_gemm_gateup(gu, (hipStream_t)stream), "gemm gate/up launch");
   if (rc) return rc;
   if (!hq_fused) {  // FP8 blocks of 128 columns span four single-wave workgroups
-    rc = dsv4_fp8_act_quant(base + w.h, R, I, 128, nullptr, base + w.ha, nullptr, base + w.hs, stream);
+    rc = dsv4_fp8_act_quant(base + w.h, Rt, I, 128, nullptr, base + w.ha, nullptr, base + w.hs, stream);
     if (rc) return rc;
   }
   Dsv4GemmArgs dn{};
@@ -383,16 +386,75 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
   dn.sorted_ids = sorted_ids;
   dn.block_expert = block_expert;
   dn.num_post_padded = npp;
-  dn.R = R;
+  dn.R = Rt;
   dn.block_m = bm;
   dn.max_blocks = w.max_blocks;
   dn.experts = table;
   dn.Kdim = I;
   dn.N = D;
   dn.out = (uint16_t*)(base + w.out);
+  if (shared) {  // h rows are indexed by flat index for every group
+    dn.has_shared = 1;
+    dn.shared_expert = E;
+    dn.shared = *shared;
+  }
   rc = hip_status(launch_moe_gemm_down(dn, (hipStream_t)stream), "gemm down launch");
   if (rc) return rc;
-  return dsv4_moe_combine(base + w.out, topk_ids, ids_int64, T, K, D, y, stream);
+  if (!shared) return dsv4_moe_combine(base + w.out, topk_ids, ids_int64, T, K, D, y, stream);
+  REQUIRE(aligned(y, 16), DSV4_ERR_SHAPE, "layer: y not 16-byte aligned");
+  const uint16_t* outp = (const uint16_t*)(base + w.out);
+  return hip_status(launch_moe_combine_flat(outp, topk_ids, ids_int64, T, K, D, (uint16_t*)y, (hipStream_t)stream,
+                                            outp + (int64_t)R * D),
+                    "combine launch");
+}
+
+int dsv4_moe_layer_workspace_bytes(int T, int K, int E, int D, int I, int profile, int64_t* bytes) {
+  REQUIRE(bytes, DSV4_ERR_NULL, "workspace: null output");
+  REQUIRE(T >= 0 && K > 0 && E > 0 && D > 0 && I > 0, DSV4_ERR_SHAPE, "workspace: bad sizes");
+  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4, DSV4_ERR_UNSUPPORTED,
+          "workspace: unknown profile %d", profile);
+  *bytes = layer_ws(T, K, E, D, I, profile).total;
+  return DSV4_OK;
+}
+
+int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
+                           const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
+                           float swiglu_limit, void* workspace, int64_t workspace_bytes, void* y, void* stream) {
+  return layer_forward(profile, scale_rule, x, topk_ids, ids_int64, topk_w, T, K, E, D, I, expert_table, nullptr,
+                       swiglu_limit, workspace, workspace_bytes, y, stream);
+}
+
+int dsv4_expand_block_scales(const void* block_scales, int64_t n_rows, int64_t k, void* out, void* stream) {
+  REQUIRE(n_rows >= 0 && k >= 0, DSV4_ERR_SHAPE, "expand scales: negative size");
+  REQUIRE(k % 32 == 0, DSV4_ERR_SHAPE, "expand scales: K=%lld not a multiple of 32", (long long)k);
+  if (n_rows == 0 || k == 0) return DSV4_OK;
+  REQUIRE(block_scales && out, DSV4_ERR_NULL, "expand scales: null pointer");
+  return hip_status(launch_expand_block_scales((const uint8_t*)block_scales, n_rows, k, (uint8_t*)out,
+                                               (hipStream_t)stream),
+                    "expand scales launch");
+}
+
+int dsv4_moe_layer_shared_workspace_bytes(int T, int K, int E, int D, int I, int64_t* bytes) {
+  REQUIRE(bytes, DSV4_ERR_NULL, "workspace: null output");
+  REQUIRE(T >= 0 && K > 0 && E > 0 && D > 0 && I > 0, DSV4_ERR_SHAPE, "workspace: bad sizes");
+  *bytes = layer_ws(T, K, E, D, I, DSV4_PROFILE_BF16, true).total;
+  return DSV4_OK;
+}
+
+int dsv4_moe_layer_forward_shared(const void* x, const void* topk_ids, int ids_int64, const float* topk_w, int T,
+                                  int K, int E, int D, int I, const void* expert_table, const void* sw1,
+                                  const void* sw1s, const void* sw3, const void* sw3s, const void* sw2,
+                                  const void* sw2s, float swiglu_limit, void* workspace, int64_t workspace_bytes,
+                                  void* y, void* stream) {
+  if (T == 0) return DSV4_OK;
+  REQUIRE(sw1 && sw1s && sw3 && sw3s && sw2 && sw2s, DSV4_ERR_NULL, "layer: null shared-expert pointer");
+  REQUIRE(aligned(sw1, 16) && aligned(sw3, 16) && aligned(sw2, 16) && aligned(sw1s, 4) && aligned(sw3s, 4) &&
+              aligned(sw2s, 4),
+          DSV4_ERR_SHAPE, "layer: misaligned shared-expert weights");
+  const Dsv4ExpertPtrs sh{(const uint8_t*)sw1, (const uint8_t*)sw1s, (const uint8_t*)sw2,
+                          (const uint8_t*)sw2s, (const uint8_t*)sw3, (const uint8_t*)sw3s};
+  return layer_forward(DSV4_PROFILE_BF16, DSV4_RULE_OCP_FLOOR, x, topk_ids, ids_int64, topk_w, T, K, E, D, I,
+                       expert_table, &sh, swiglu_limit, workspace, workspace_bytes, y, stream);
 }
 
 }  // extern "C"

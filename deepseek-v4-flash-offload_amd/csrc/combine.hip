@@ -64,11 +64,15 @@ DSV4_DEV int wave_select_rank(int rank, int n, int r) {
 }
 
 // Workgroups of 64 lanes tile (token, 512-column chunk); each lane owns 8
-// columns. The token's K entries are visited in (expert id, k) order.
+// columns. The token's K entries are visited in (expert id, k) order. With
+// shared rows (the shared expert's output, bf16 [T, D]) the routed sum is
+// rounded to bf16 first and the shared row added to it, as the reference's
+// `out + self.shared_experts(hs)` adds two bf16 tensors (deepseek_v4.py:262-264).
 template <typename IdT>
 __global__ __launch_bounds__(64) void combine_flat_kernel(const u32x4* __restrict__ src,
                                                           const IdT* __restrict__ ids, int K, int D,
-                                                          u32x4* __restrict__ y) {
+                                                          u32x4* __restrict__ y,
+                                                          const u32x4* __restrict__ shared_rows) {
   const int t = blockIdx.y;
   const int lane = threadIdx.x;
   const long long key = lane < K ? (long long)ids[(int64_t)t * K + lane] : 0;
@@ -80,7 +84,22 @@ __global__ __launch_bounds__(64) void combine_flat_kernel(const u32x4* __restric
     const int k = wave_select_rank(rank, K, r);
     if (c < vecs) accumulate8(acc, src[((int64_t)t * K + k) * vecs + c]);
   }
-  if (c < vecs) y[(int64_t)t * vecs + c] = pack8(acc);
+  if (c >= vecs) return;
+  if (shared_rows) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = dsv4::bf16_to_f32(dsv4::f32_to_bf16(acc[i]));
+    accumulate8(acc, shared_rows[(int64_t)t * vecs + c]);
+  }
+  y[(int64_t)t * vecs + c] = pack8(acc);
+}
+
+__global__ __launch_bounds__(256) void expand_block_scales_kernel(const uint8_t* __restrict__ block, int64_t N,
+                                                                  int64_t K32, int64_t KB,
+                                                                  uint8_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= N * K32) return;
+  const int64_t n = i / K32, k = i - n * K32;
+  out[i] = block[(n / 128) * KB + k / 4];
 }
 
 __global__ __launch_bounds__(256) void bucket_rows_kernel(const int32_t* __restrict__ row, int R, int T, int Kmax,
@@ -135,15 +154,24 @@ hipError_t launch_moe_gather_rows(const uint8_t* src, int64_t n_src, const int32
 }
 
 hipError_t launch_moe_combine_flat(const uint16_t* src, const void* topk_ids, int ids_int64, int T, int K,
-                                   int D, uint16_t* y, hipStream_t st) {
+                                   int D, uint16_t* y, hipStream_t st, const uint16_t* shared_rows) {
   if (T == 0 || D == 0) return hipSuccess;
   const dim3 grid((D / 8 + 63) / 64, T);
   if (ids_int64)
     hipLaunchKernelGGL(combine_flat_kernel<long long>, grid, dim3(64), 0, st, (const u32x4*)src,
-                       (const long long*)topk_ids, K, D, (u32x4*)y);
+                       (const long long*)topk_ids, K, D, (u32x4*)y, (const u32x4*)shared_rows);
   else
     hipLaunchKernelGGL(combine_flat_kernel<int32_t>, grid, dim3(64), 0, st, (const u32x4*)src,
-                       (const int32_t*)topk_ids, K, D, (u32x4*)y);
+                       (const int32_t*)topk_ids, K, D, (u32x4*)y, (const u32x4*)shared_rows);
+  return hipGetLastError();
+}
+
+hipError_t launch_expand_block_scales(const uint8_t* block, int64_t N, int64_t K, uint8_t* out, hipStream_t st) {
+  const int64_t K32 = K / 32, KB = (K + 127) / 128, total = N * K32;
+  if (total == 0) return hipSuccess;
+  if ((total + 255) / 256 > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(expand_block_scales_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, block, N,
+                     K32, KB, out);
   return hipGetLastError();
 }
 

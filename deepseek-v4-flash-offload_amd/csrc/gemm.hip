@@ -36,6 +36,8 @@
 //             [64+16g, 64+16g+16) in bytes 16-31.
 //   scales  : lane (r, g) supplies the E8M0 of logical block g of its row/col.
 //   C       : lane l holds C[4*(l/16)+i][l%16], i = 0..3.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 #include "quant_dev.h"
@@ -73,10 +75,17 @@ struct AStage<1> {  // E2M1: 16 bytes per lane per MFMA
   v4i d[2];
   uint32_t s;
 };
-struct BStage {
-  v4i d[kNT][2];
-  uint32_t s[kNT];
+// B operand of one stage: E2M1 weights (16 bytes per lane per MFMA, kNT tiles)
+// or, for the shared expert, E4M3 weights (32 bytes, laid out like the E4M3 A
+// operand). An E4M3 stage holds kNT/2 tiles, so both take the same registers;
+// the E4M3 path covers its kNT tiles in two passes over K.
+template <bool B8>
+struct BStageT {
+  static constexpr int NTB = B8 ? kNT / 2 : kNT;
+  typename std::conditional<B8, v8i, v4i>::type d[NTB][2];
+  uint32_t s[NTB];
 };
+using BStage = BStageT<false>;
 
 // Every operand lives in global memory; the casts keep the loads global_load_*
 // (pointers read from the expert table would otherwise become flat accesses).
@@ -168,19 +177,38 @@ DSV4_DEV void load_a(AStage<AFMT>& a, const uint8_t* abase, const uint8_t* asbas
   if constexpr (SCALES) a.s = ld_u16(asbase + j * 8 + 2 * g);
 }
 
-template <bool SCALES = true>
-DSV4_DEV void load_b(BStage& b, const uint8_t* const* bt, const uint8_t* const* bst, int j, int g) {
+template <bool SCALES = true, bool B8 = false>
+DSV4_DEV void load_b(BStageT<B8>& b, const uint8_t* const* bt, const uint8_t* const* bst, int j, int g) {
 #pragma unroll
-  for (int t = 0; t < kNT; ++t) {
-    const uint8_t* p = bt[t] + (int64_t)j * 128 + g * 32;
-    b.d[t][0] = ld16_stream(p);
-    b.d[t][1] = ld16_stream(p + 16);
+  for (int t = 0; t < BStageT<B8>::NTB; ++t) {
+    if constexpr (B8) {  // E4M3 rows: the E4M3 A layout (two 16-byte halves per MFMA)
+      const uint8_t* p = bt[t] + (int64_t)j * 256 + 16 * (g & 1) + 64 * (g >> 1);
+#pragma unroll
+      for (int ji = 0; ji < 2; ++ji) {
+        const v4i lo = ld16_stream(p + 32 * ji);
+        const v4i hi = ld16_stream(p + 32 * ji + 128);
+        b.d[t][ji] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+      }
+    } else {
+      const uint8_t* p = bt[t] + (int64_t)j * 128 + g * 32;
+      b.d[t][0] = ld16_stream(p);
+      b.d[t][1] = ld16_stream(p + 16);
+    }
     if constexpr (SCALES) b.s[t] = ld_u16(bst[t] + j * 8 + 2 * g);
   }
 }
 
-template <int AFMT>
-DSV4_DEV void compute(v4f* acc, const AStage<AFMT>& a, const BStage& b) {
+template <bool B8>
+DSV4_DEV v8i b_operand(const BStageT<B8>& b, int t, int ji) {
+  if constexpr (B8) {
+    return b.d[t][ji];
+  } else {
+    return v8i{b.d[t][ji].x, b.d[t][ji].y, b.d[t][ji].z, b.d[t][ji].w, 0, 0, 0, 0};
+  }
+}
+
+template <int AFMT, bool B8 = false>
+DSV4_DEV void compute(v4f* acc, const AStage<AFMT>& a, const BStageT<B8>& b) {
 #pragma unroll
   for (int ji = 0; ji < 2; ++ji) {
     v8i av;
@@ -191,19 +219,30 @@ DSV4_DEV void compute(v4f* acc, const AStage<AFMT>& a, const BStage& b) {
     }
     const int sa = (int)((a.s >> (8 * ji)) & 0xffu);
 #pragma unroll
-    for (int t = 0; t < kNT; ++t) {
-      const v8i bv = v8i{b.d[t][ji].x, b.d[t][ji].y, b.d[t][ji].z, b.d[t][ji].w, 0, 0, 0, 0};
+    for (int t = 0; t < BStageT<B8>::NTB; ++t) {
+      const v8i bv = b_operand<B8>(b, t, ji);
       const int sb = (int)((b.s[t] >> (8 * ji)) & 0xffu);
-      acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc[t], AFMT == 0 ? 0 : 4, 4, 0, sa, 0, sb);
+      acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc[t], AFMT == 0 ? 0 : 4, B8 ? 0 : 4, 0,
+                                                                sa, 0, sb);
     }
   }
+}
+
+// A row of flat index f: a routed entry reads row f / a_row_div, one of the
+// trailing shared_a_rows shared-expert entries row f - (R - shared_a_rows), and
+// padding (f >= R) row 0 (its products land only in rows that are never stored).
+template <bool SH>
+DSV4_DEV int64_t a_row(const Dsv4GemmArgs& p, int f) {
+  if constexpr (!SH) return f < p.R ? (int64_t)(f / p.a_row_div) : 0;
+  const int r0 = p.R - p.shared_a_rows;
+  return f < r0 ? (int64_t)(f / p.a_row_div) : (f < p.R ? (int64_t)(f - r0) : 0);
 }
 
 // Epilogue of one 16-row subtile: lane holds rows row0 + 4*g + i (i = 0..3) of
 // column r16 of each of the 4 tiles. Gate/up: hb receives the bf16 h values the
 // SwiGLU produced (tiles t = 0, 1 are intermediate columns col0 + 16 t + r16) and
 // fr the rows' flat indices; h is written unless the caller fuses its quantisation.
-template <bool GATEUP>
+template <bool GATEUP, bool SH = false>
 DSV4_DEV void store_tile(const Dsv4GemmArgs& p, const v4f* acc, int row0, int col0, int g, int r16,
                          uint32_t (*hb)[2] = nullptr, int* fr = nullptr) {
 #pragma unroll
@@ -214,7 +253,8 @@ DSV4_DEV void store_tile(const Dsv4GemmArgs& p, const v4f* acc, int row0, int co
     uint16_t* orow = p.out + (int64_t)f * p.N + col0 + r16;
     if (GATEUP) {
       // deepseek_v4.py:177-187: bf16 GEMM outputs -> fp32, clamp, silu(gate) * up * w
-      const float w = p.topk_w[f];
+      // (shared-expert rows: w = 1, model_npu.py:478-489 applies no weight)
+      const float w = (!SH || f < p.R - p.shared_a_rows) ? p.topk_w[f] : 1.0f;
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         float gt = dsv4::bf16_to_f32(dsv4::f32_to_bf16(acc[t][i]));
@@ -261,26 +301,28 @@ DSV4_DEV void quantise_h_mxfp4(const Dsv4GemmArgs& p, const uint32_t (*hb)[2], c
   }
 }
 
-template <int AFMT, bool GATEUP, int NST>
+// SH: the launch includes the shared expert's E4M3 blocks (a separate
+// instantiation, so the routed-only kernels keep their register budget).
+template <int AFMT, bool GATEUP, int NST, bool SH>
 __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int mb = blockIdx.y;
   if (mb * kBM >= p.num_post_padded[0]) return;
   const int e = p.block_expert[mb];
-  const Dsv4ExpertPtrs ex = p.experts[e];
+  // the shared expert's blocks carry id shared_expert and read its E4M3 weights
+  const bool shared = SH && e == p.shared_expert;
+  const Dsv4ExpertPtrs ex = shared ? p.shared : p.experts[e];
   // an expert whose weights are not in the table contributes zeros (never read null)
   const bool have_w = GATEUP ? (ex.w1p && ex.w1s && ex.w3p && ex.w3s) : (ex.w2p && ex.w2s);
   const int r16 = lane & 15, g = lane >> 4;
 
-  // A operand row of this lane, gathered on load. Padding rows read row 0:
-  // their products land only in output rows that are never stored.
-  const int f_in = p.sorted_ids[mb * kBM + r16];
-  const int64_t arow = f_in < p.R ? (int64_t)(f_in / p.a_row_div) : 0;
+  // A operand row of this lane, gathered on load
+  const int64_t arow = a_row<SH>(p, p.sorted_ids[mb * kBM + r16]);
   const uint8_t* abase = p.a + arow * p.a_row_bytes;
   const uint8_t* asbase = p.a_scale + arow * (int64_t)(p.Kdim / 32);
 
-  // weight rows of this lane's tiles
-  const int64_t brow_bytes = p.Kdim / 2, bsrow = p.Kdim / 32;
+  // weight rows of this lane's tiles (E2M1: K/2 bytes per row, E4M3: K)
+  const int64_t brow_bytes = shared ? p.Kdim : p.Kdim / 2, bsrow = p.Kdim / 32;
   int col0;
   const uint8_t* bt[kNT];
   const uint8_t* bst[kNT];
@@ -308,46 +350,64 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
 #pragma unroll
   for (int t = 0; t < kNT; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  if (have_w) {
-    // NST = Kdim / 256 stages, fully unrolled into straight-line code. With
-    // DSV4_GEMM_PREFETCH = P > 0 the loads of stage j+P are issued before the
-    // MFMAs of stage j and a scheduling barrier keeps them there (a P+1 deep
-    // register ring); with P = 0 the compiler schedules freely.
+  // NST = Kdim / 256 stages, fully unrolled into straight-line code. With
+  // DSV4_GEMM_PREFETCH = P > 0 the loads of stage j+P are issued before the
+  // MFMAs of stage j and a scheduling barrier keeps them there (a P+1 deep
+  // register ring); with P = 0 the compiler schedules freely.
+  // T0: first tile of this pass (E4M3 weights: two passes of kNT/2 tiles).
+  auto kloop = [&](auto b8, auto t0c) {
+    constexpr bool B8 = decltype(b8)::value;
+    constexpr int t0 = decltype(t0c)::value;
+    constexpr int NTB = BStageT<B8>::NTB;
     constexpr int P = DSV4_GEMM_PREFETCH;
     constexpr int RING = P + 1;
+    const uint8_t* const* btp = bt + t0;
+    const uint8_t* const* bstp = bst + t0;
     AStage<AFMT> a[RING];
-    BStage b[RING];
-    RowScales<NST> as_row, bs_row[kNT];
+    BStageT<B8> b[RING];
+    RowScales<NST> as_row, bs_row[NTB];
     load_row_scales<NST>(as_row, asbase, g);
 #pragma unroll
-    for (int t = 0; t < kNT; ++t) load_row_scales<NST>(bs_row[t], bst[t], g);
+    for (int t = 0; t < NTB; ++t) load_row_scales<NST>(bs_row[t], bstp[t], g);
 #pragma unroll
     for (int j = 0; j < P && j < NST; ++j) {
       load_a<AFMT, false>(a[j % RING], abase, asbase, j, g);
-      load_b<false>(b[j % RING], bt, bst, j, g);
+      load_b<false, B8>(b[j % RING], btp, bstp, j, g);
     }
 #pragma unroll
     for (int j = 0; j < NST; ++j) {
       if (j + P < NST) {
         load_a<AFMT, false>(a[(j + P) % RING], abase, asbase, j + P, g);
-        load_b<false>(b[(j + P) % RING], bt, bst, j + P, g);
+        load_b<false, B8>(b[(j + P) % RING], btp, bstp, j + P, g);
       }
       if constexpr (P > 0) __builtin_amdgcn_sched_barrier(0);
       a[j % RING].s = stage_scales<NST>(as_row, j, r16, g);
 #pragma unroll
-      for (int t = 0; t < kNT; ++t) b[j % RING].s[t] = stage_scales<NST>(bs_row[t], j, r16, g);
-      compute<AFMT>(acc, a[j % RING], b[j % RING]);
+      for (int t = 0; t < NTB; ++t) b[j % RING].s[t] = stage_scales<NST>(bs_row[t], j, r16, g);
+      compute<AFMT, B8>(acc + t0, a[j % RING], b[j % RING]);
       if constexpr (P > 0) __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  if (have_w) {
+    if constexpr (AFMT == 0 && SH) {  // E4M3 weights only meet E4M3 activations (bf16 profile)
+      if (shared) {
+        kloop(std::true_type{}, std::integral_constant<int, 0>{});
+        kloop(std::true_type{}, std::integral_constant<int, kNT / 2>{});
+      } else {
+        kloop(std::false_type{}, std::integral_constant<int, 0>{});
+      }
+    } else {
+      kloop(std::false_type{}, std::integral_constant<int, 0>{});
     }
   }
 
   if (GATEUP && p.hq_mode == 2) {  // MXFP4 h: this wave holds whole 32-column blocks
     uint32_t hb[4][2];
     int fr[4];
-    store_tile<GATEUP>(p, acc, mb * kBM, col0, g, r16, hb, fr);
+    store_tile<GATEUP, SH>(p, acc, mb * kBM, col0, g, r16, hb, fr);
     quantise_h_mxfp4(p, hb, fr, col0, g, r16);
   } else {
-    store_tile<GATEUP>(p, acc, mb * kBM, col0, g, r16);
+    store_tile<GATEUP, SH>(p, acc, mb * kBM, col0, g, r16);
   }
 }
 
@@ -361,9 +421,11 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
 // tiles) is a multiple of 8, so all M blocks of one (expert, N tile) land on the
 // same XCD and re-read the weight tile from its L2.
 // ---------------------------------------------------------------------------
-template <int AFMT, int MT>
+// T0: first of the accumulator tiles this B stage feeds (E4M3 passes: 0, kNT/2)
+template <int AFMT, int MT, bool B8 = false, int T0 = 0>
 DSV4_DEV void compute_tiled(v4f (*acc)[kNT], const uint8_t* lds, const uint8_t* as_tab, int as_pitch, int j,
-                            const BStage& b, int r16, int g) {
+                            const BStageT<B8>& b, int r16, int g) {
+  constexpr int t0 = T0;
   constexpr int ASB = AFMT == 0 ? 256 : 128;
   constexpr int AROW = ASB + 16;
 #pragma unroll
@@ -384,17 +446,18 @@ DSV4_DEV void compute_tiled(v4f (*acc)[kNT], const uint8_t* lds, const uint8_t* 
       }
       const int sa = as_tab[row * as_pitch + 8 * j + 2 * g + ji];
 #pragma unroll
-      for (int t = 0; t < kNT; ++t) {
-        const v8i bv = v8i{b.d[t][ji].x, b.d[t][ji].y, b.d[t][ji].z, b.d[t][ji].w, 0, 0, 0, 0};
+      for (int t = 0; t < BStageT<B8>::NTB; ++t) {
+        const v8i bv = b_operand<B8>(b, t, ji);
         const int sb = (int)((b.s[t] >> (8 * ji)) & 0xffu);
-        acc[mt][t] =
-            __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc[mt][t], AFMT == 0 ? 0 : 4, 4, 0, sa, 0, sb);
+        acc[mt][t0 + t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc[mt][t0 + t],
+                                                                           AFMT == 0 ? 0 : 4, B8 ? 0 : 4, 0, sa, 0,
+                                                                           sb);
       }
     }
   }
 }
 
-template <int AFMT, bool GATEUP, int NST, int MT, int NW>
+template <int AFMT, bool GATEUP, int NST, int MT, int NW, bool SH>
 __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gemm_tiled_kernel(Dsv4GemmArgs p) {
   constexpr int BM = 16 * MT;
   constexpr int NTH = 64 * NW;                // threads per workgroup
@@ -413,7 +476,8 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
   const int mb = blockIdx.y;
   if (mb * BM >= p.num_post_padded[0]) return;
   const int e = p.block_expert[mb];
-  const Dsv4ExpertPtrs ex = p.experts[e];
+  const bool shared = SH && e == p.shared_expert;
+  const Dsv4ExpertPtrs ex = shared ? p.shared : p.experts[e];
   const bool have_w = GATEUP ? (ex.w1p && ex.w1s && ex.w3p && ex.w3s) : (ex.w2p && ex.w2s);
   const int r16 = lane & 15, g = lane >> 4;
 
@@ -426,13 +490,12 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
 #pragma unroll
   for (int v = 0; v < LV; ++v) {
     const int id = (v * NW + wave) * 64 + lane, row = id / CPRW, ch = id % CPRW;
-    const int f = p.sorted_ids[mb * BM + row];
-    const int64_t ar = f < p.R ? (int64_t)(f / p.a_row_div) : 0;  // padding rows read row 0
+    const int64_t ar = a_row<SH>(p, p.sorted_ids[mb * BM + row]);
     lsrc[v] = p.a + ar * p.a_row_bytes + 16 * ch;
     ldst[v] = row * AROW + 16 * ch;
   }
 
-  const int64_t brow_bytes = p.Kdim / 2, bsrow = p.Kdim / 32;
+  const int64_t brow_bytes = shared ? p.Kdim : p.Kdim / 2, bsrow = p.Kdim / 32;
   int col0;
   const uint8_t* bt[kNT];
   const uint8_t* bst[kNT];
@@ -462,27 +525,32 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
 #pragma unroll
     for (int t = 0; t < kNT; ++t) acc[mt][t] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  if (have_w) {  // uniform per workgroup, so the barriers below are reached by all
+  // uniform per workgroup (have_w, shared), so the barriers inside are reached by all
+  auto kloop = [&](auto b8, auto t0c) {
+    constexpr bool B8 = decltype(b8)::value;
+    constexpr int t0 = decltype(t0c)::value;
+    constexpr int NTB = BStageT<B8>::NTB;
+    const uint8_t* const* btp = bt + t0;
+    const uint8_t* const* bstp = bst + t0;
     // scales of the whole K range, loaded once: the weight rows' by their lanes
     // (shared out per stage by permutes), the A rows' into an LDS table
-    RowScales<NST> bs_row[kNT];
+    RowScales<NST> bs_row[NTB];
 #pragma unroll
-    for (int t = 0; t < kNT; ++t) load_row_scales<NST>(bs_row[t], bst[t], g);
+    for (int t = 0; t < NTB; ++t) load_row_scales<NST>(bs_row[t], bstp[t], g);
 #pragma unroll
     for (int i = 0; i < (AS_CHUNKS + NTH - 1) / NTH; ++i) {
       const int c = i * NTH + tid;
       if (c < AS_CHUNKS) {
         const int row = c / (KSB / 16), ch = c % (KSB / 16);
-        const int f = p.sorted_ids[mb * BM + row];
-        const int64_t ar = f < p.R ? (int64_t)(f / p.a_row_div) : 0;
+        const int64_t ar = a_row<SH>(p, p.sorted_ids[mb * BM + row]);
         *(v4i*)&as_tab[row * ASP + 16 * ch] = ld16(p.a_scale + ar * KSB + 16 * ch);
       }
     }
     v4i lreg[LV];
-    BStage b[2];
+    BStageT<B8> b[2];
 #pragma unroll
     for (int v = 0; v < LV; ++v) lreg[v] = ld16(lsrc[v]);
-    load_b<false>(b[0], bt, bst, 0, g);
+    load_b<false, B8>(b[0], btp, bstp, 0, g);
 #pragma unroll
     for (int v = 0; v < LV; ++v) *(v4i*)&a_lds[0][ldst[v]] = lreg[v];
     __syncthreads();
@@ -491,12 +559,12 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
       if (j + 1 < NST) {
 #pragma unroll
         for (int v = 0; v < LV; ++v) lreg[v] = ld16(lsrc[v] + (j + 1) * ASB);
-        load_b<false>(b[(j + 1) & 1], bt, bst, j + 1, g);
+        load_b<false, B8>(b[(j + 1) & 1], btp, bstp, j + 1, g);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int t = 0; t < kNT; ++t) b[j & 1].s[t] = stage_scales<NST>(bs_row[t], j, r16, g);
-      compute_tiled<AFMT, MT>(acc, a_lds[j & 1], as_tab, ASP, j, b[j & 1], r16, g);
+      for (int t = 0; t < NTB; ++t) b[j & 1].s[t] = stage_scales<NST>(bs_row[t], j, r16, g);
+      compute_tiled<AFMT, MT, B8, t0>(acc, a_lds[j & 1], as_tab, ASP, j, b[j & 1], r16, g);
       __builtin_amdgcn_sched_barrier(0);
       if (j + 1 < NST) {
 #pragma unroll
@@ -504,13 +572,27 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
       }
       __syncthreads();
     }
+  };
+  if (have_w) {
+    if constexpr (AFMT == 0 && SH) {
+      if (shared) {
+        kloop(std::true_type{}, std::integral_constant<int, 0>{});
+        // the second pass restages the A tiles: the LDS ring is free again
+        kloop(std::true_type{}, std::integral_constant<int, kNT / 2>{});
+      } else {
+        kloop(std::false_type{}, std::integral_constant<int, 0>{});
+      }
+    } else {
+      kloop(std::false_type{}, std::integral_constant<int, 0>{});
+    }
   }
 
   if (GATEUP && p.hq_mode) {
     uint32_t hb[MT][4][2];
     int fr[MT][4];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) store_tile<GATEUP>(p, acc[mt], mb * BM + 16 * mt, col0, g, r16, hb[mt], fr[mt]);
+    for (int mt = 0; mt < MT; ++mt)
+      store_tile<GATEUP, SH>(p, acc[mt], mb * BM + 16 * mt, col0, g, r16, hb[mt], fr[mt]);
     if (p.hq_mode == 2) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) quantise_h_mxfp4(p, hb[mt], fr[mt], col0, g, r16);
@@ -547,21 +629,21 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
     }
   } else {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) store_tile<GATEUP>(p, acc[mt], mb * BM + 16 * mt, col0, g, r16);
+    for (int mt = 0; mt < MT; ++mt) store_tile<GATEUP, SH>(p, acc[mt], mb * BM + 16 * mt, col0, g, r16);
   }
 }
 
 }  // namespace
 
-template <bool GATEUP, int NST>
-static void launch_nst(const Dsv4GemmArgs& a, hipStream_t st) {
+template <bool GATEUP, int NST, bool SH>
+static void launch_nst_sh(const Dsv4GemmArgs& a, hipStream_t st) {
   const int cols_per_wave = GATEUP ? 32 : 64;
   if (a.block_m == kBM) {  // decode-shaped: single-wave workgroups
     const dim3 grid(a.N / (kWaves * cols_per_wave), a.max_blocks);
     if (a.afmt == 0)
-      hipLaunchKernelGGL((moe_gemm_kernel<0, GATEUP, NST>), grid, dim3(64 * kWaves), 0, st, a);
+      hipLaunchKernelGGL((moe_gemm_kernel<0, GATEUP, NST, SH>), grid, dim3(64 * kWaves), 0, st, a);
     else
-      hipLaunchKernelGGL((moe_gemm_kernel<1, GATEUP, NST>), grid, dim3(64 * kWaves), 0, st, a);
+      hipLaunchKernelGGL((moe_gemm_kernel<1, GATEUP, NST, false>), grid, dim3(64 * kWaves), 0, st, a);
     return;
   }
   // 4-wave workgroups (8-wave ones, sharing each A tile across twice the
@@ -569,15 +651,25 @@ static void launch_nst(const Dsv4GemmArgs& a, hipStream_t st) {
   const dim3 grid(a.N / (4 * cols_per_wave), a.max_blocks);
   if (a.block_m == 64) {
     if (a.afmt == 0)
-      hipLaunchKernelGGL((moe_gemm_tiled_kernel<0, GATEUP, NST, 4, 4>), grid, dim3(256), 0, st, a);
+      hipLaunchKernelGGL((moe_gemm_tiled_kernel<0, GATEUP, NST, 4, 4, SH>), grid, dim3(256), 0, st, a);
     else
-      hipLaunchKernelGGL((moe_gemm_tiled_kernel<1, GATEUP, NST, 4, 4>), grid, dim3(256), 0, st, a);
+      hipLaunchKernelGGL((moe_gemm_tiled_kernel<1, GATEUP, NST, 4, 4, false>), grid, dim3(256), 0, st, a);
   } else {
     if (a.afmt == 0)
-      hipLaunchKernelGGL((moe_gemm_tiled_kernel<0, GATEUP, NST, 8, 4>), grid, dim3(256), 0, st, a);
+      hipLaunchKernelGGL((moe_gemm_tiled_kernel<0, GATEUP, NST, 8, 4, SH>), grid, dim3(256), 0, st, a);
     else
-      hipLaunchKernelGGL((moe_gemm_tiled_kernel<1, GATEUP, NST, 8, 4>), grid, dim3(256), 0, st, a);
+      hipLaunchKernelGGL((moe_gemm_tiled_kernel<1, GATEUP, NST, 8, 4, false>), grid, dim3(256), 0, st, a);
   }
+}
+
+// The shared-expert instantiations exist for E4M3 activations (the bf16
+// profile) only; the C ABI rejects a shared expert with E2M1 activations.
+template <bool GATEUP, int NST>
+static void launch_nst(const Dsv4GemmArgs& a, hipStream_t st) {
+  if (a.has_shared && a.afmt == 0)
+    launch_nst_sh<GATEUP, NST, true>(a, st);
+  else
+    launch_nst_sh<GATEUP, NST, false>(a, st);
 }
 
 template <bool GATEUP>

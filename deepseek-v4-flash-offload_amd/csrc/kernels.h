@@ -40,18 +40,22 @@ hipError_t launch_moe_align(const void* topk_ids, int ids_int64, const float* to
                             int E, int block_m, int max_blocks, const Dsv4AlignOut& o, hipStream_t st);
 
 // align (workgroup 0) and activation quantisation (workgroups 1..) in one launch;
-// qfmt 0 = FP8 per-128 codes + E8M0 x4 scales, 1 = MXFP4 per-32 (rule 0/1)
+// qfmt 0 = FP8 per-128 codes + E8M0 x4 scales, 1 = MXFP4 per-32 (rule 0/1).
+// n_shared > 0 appends a group of n_shared rows (flat indices R..) with
+// block_expert E after the routed experts; the padding sentinel becomes R + n_shared.
 hipError_t launch_moe_align_quant(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K, int E,
                                   int block_m, int max_blocks, const Dsv4AlignOut& o, const uint16_t* x,
                                   int64_t n_elems, int qfmt, int rule, void* q_codes, void* q_scale,
-                                  hipStream_t st);
+                                  hipStream_t st, int n_shared = 0);
 hipError_t launch_moe_gather_rows(const uint8_t* src, int64_t n_src, const int32_t* row, int64_t n_rows,
                                   int64_t row_bytes, uint8_t* dst, hipStream_t st);
 // y[t] = bf16( sum over the token's entries, ordered by key, of rows of `src` (bf16) )
 // mode 0: entry (t,k) -> src row t*K+k, key = topk_ids[t,k]   (flat-order combine)
 // mode 1: entries from a per-token position list built from `row`, key = position
 hipError_t launch_moe_combine_flat(const uint16_t* src, const void* topk_ids, int ids_int64, int T, int K,
-                                   int D, uint16_t* y, hipStream_t st);
+                                   int D, uint16_t* y, hipStream_t st, const uint16_t* shared_rows = nullptr);
+// out[n][k/32] = block[n/128][k/128]: 128x128 E8M0 block scales repeated per 32 along K
+hipError_t launch_expand_block_scales(const uint8_t* block, int64_t N, int64_t K, uint8_t* out, hipStream_t st);
 hipError_t launch_moe_unpermute_rows(const uint16_t* src, const int32_t* row, int R, int T, int Kmax, int D,
                                      int32_t* work_cnt, int32_t* work_pos, int32_t* status, uint16_t* y,
                                      hipStream_t st);
@@ -83,6 +87,15 @@ struct Dsv4GemmArgs {
   int hq_skip_h;
   uint8_t* hq_codes;
   uint8_t* hq_scale;
+  // ---- shared expert as one more group (zero = none; E4M3 activations only).
+  //   M blocks whose block_expert is shared_expert read `shared`: E4M3 weights
+  //   w1/w3 [N, K] / w2 [D, I] with E8M0 per 32 along K ([N, K/32], the 128x128
+  //   block scales repeated). The last shared_a_rows flat indices below R are
+  //   shared-expert rows: A row f - (R - shared_a_rows), routing weight 1.
+  int has_shared;
+  int shared_expert;
+  int shared_a_rows;
+  Dsv4ExpertPtrs shared;
 };
 hipError_t launch_moe_gemm_gateup(const Dsv4GemmArgs& a, hipStream_t st);
 hipError_t launch_moe_gemm_down(const Dsv4GemmArgs& a, hipStream_t st);

@@ -315,6 +315,33 @@ def gemm_down(afmt, a, a_scale, al: AlignResult, table, I, D):
     return out
 
 
+def expand_block_scales(block_scales: torch.Tensor, n_rows: int, k: int) -> torch.Tensor:
+    """128x128-block E8M0 scales [ceil(n/128), ceil(k/128)] -> per-32 layout [n, k/32]."""
+    b = _u8(_dev(block_scales, "expand_block_scales"))
+    if b.shape != ((n_rows + 127) // 128, (k + 127) // 128):
+        raise ValueError(f"expand_block_scales: scales {tuple(b.shape)} do not tile a [{n_rows}, {k}] weight")
+    out = torch.empty(n_rows, k // 32, dtype=torch.uint8, device=b.device)
+    call("dsv4_expand_block_scales", _p(b), n_rows, k, _p(out), _stream(b))
+    return out
+
+
+def prepare_shared_expert(w1, w1s, w3, w3s, w2, w2s):
+    """The shared expert's FP8 checkpoint tensors (``w{1,3}`` [I, D], ``w2`` [D, I]
+    E4M3, 128x128 E8M0 block scales) on the device in the layout
+    ``dsv4_moe_layer_forward_shared`` reads: codes as bytes, scales per 32."""
+    out = {}
+    for name, w, sc in (("w1", w1, w1s), ("w3", w3, w3s), ("w2", w2, w2s)):
+        codes = w.contiguous().view(torch.uint8) if w.dtype != torch.uint8 else w.contiguous()
+        _dev(codes, "prepare_shared_expert")
+        n, k = codes.shape
+        out[name] = codes
+        out[name + "s"] = expand_block_scales(sc, n, k)
+    I, D = out["w1"].shape
+    if out["w3"].shape != (I, D) or out["w2"].shape != (D, I):
+        raise ValueError("prepare_shared_expert: w1/w3 must be [I, D] and w2 [D, I]")
+    return out
+
+
 class LayerRunner:
     """Holds a reusable workspace for ``dsv4_moe_layer_forward`` (one routed layer)."""
 
@@ -323,15 +350,21 @@ class LayerRunner:
         self.E, self.D, self.I = n_experts, hidden, inter
         self._ws = None
 
-    def workspace(self, T, K, profile):
+    def workspace(self, T, K, profile, shared=False):
         n = ctypes.c_int64(0)
-        call("dsv4_moe_layer_workspace_bytes", T, K, self.E, self.D, self.I, profile, ctypes.byref(n))
+        if shared:
+            call("dsv4_moe_layer_shared_workspace_bytes", T, K, self.E, self.D, self.I, ctypes.byref(n))
+        else:
+            call("dsv4_moe_layer_workspace_bytes", T, K, self.E, self.D, self.I, profile, ctypes.byref(n))
         if self._ws is None or self._ws.numel() < n.value:
             self._ws = torch.empty(max(n.value, 256), dtype=torch.uint8, device=self.device)
         return self._ws
 
     def forward(self, x, topk_ids, topk_w, table, profile=_lib.PROFILE_BF16, rule=_lib.RULE_OCP_FLOOR,
-                swiglu_limit=10.0, out=None):
+                swiglu_limit=10.0, out=None, shared=None):
+        """The routed layer; with ``shared`` (``prepare_shared_expert``) the shared
+        expert runs as one more group of the same launches and is added to the
+        routed output (bf16 profile only)."""
         _dev(x, "layer_forward")
         if x.dtype != torch.bfloat16 or not x.is_contiguous():
             raise TypeError("layer_forward: contiguous bf16 activations required")
@@ -339,9 +372,18 @@ class LayerRunner:
         ids = topk_ids.contiguous()
         K = ids.shape[1]
         w = topk_w.to(torch.float32).contiguous()
-        ws = self.workspace(T, K, profile)
         y = out if out is not None else torch.empty((T, D), dtype=torch.bfloat16, device=x.device)
-        call("dsv4_moe_layer_forward", profile, rule, _p(x), _p(ids), 1 if ids.dtype == torch.int64 else 0,
-             _p(w), T, K, self.E, D, self.I, _p(table), float(swiglu_limit or 0.0), _p(ws), ws.numel(), _p(y),
-             _stream(x))
+        i64 = 1 if ids.dtype == torch.int64 else 0
+        lim = float(swiglu_limit or 0.0)
+        if shared is not None:
+            if profile != _lib.PROFILE_BF16:
+                raise ValueError("layer_forward: the shared expert is fused in the bf16 profile only")
+            ws = self.workspace(T, K, profile, shared=True)
+            call("dsv4_moe_layer_forward_shared", _p(x), _p(ids), i64, _p(w), T, K, self.E, D, self.I, _p(table),
+                 _p(shared["w1"]), _p(shared["w1s"]), _p(shared["w3"]), _p(shared["w3s"]), _p(shared["w2"]),
+                 _p(shared["w2s"]), lim, _p(ws), ws.numel(), _p(y), _stream(x))
+            return y
+        ws = self.workspace(T, K, profile)
+        call("dsv4_moe_layer_forward", profile, rule, _p(x), _p(ids), i64, _p(w), T, K, self.E, D, self.I,
+             _p(table), lim, _p(ws), ws.numel(), _p(y), _stream(x))
         return y

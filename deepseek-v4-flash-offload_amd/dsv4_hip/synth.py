@@ -7,7 +7,9 @@ Distributions (same for every config):
   * expert ids: Zipf(s=1.1) over expert ranks, a seeded rank -> expert
     permutation, K distinct experts per token drawn by Gumbel-top-k
     (Plackett-Luce sampling without replacement);
-  * routing weights: softmax of N(0, 1) logits over the K picks (fp32).
+  * routing weights: softmax of N(0, 1) logits over the K picks (fp32);
+  * shared expert: N(0, 2^-6) weights block-quantised to E4M3 with 128x128
+    E8M0 scales 2^ceil(log2(amax / 448)) (the checkpoint's FP8 form).
 
 Seeds: config-0 matrix rng(0) bytes / rng(1) scales / rng(2) x; experts
 rng(100 + e); rank permutation rng(3); Gumbel noise rng(4); routing logits
@@ -33,6 +35,31 @@ def expert_weights(e, hidden, inter):
     w3p, w3s = packed_weight(rng, inter, hidden)
     w2p, w2s = packed_weight(rng, hidden, inter)
     return {"w1p": w1p, "w1s": w1s, "w2p": w2p, "w2s": w2s, "w3p": w3p, "w3s": w3s}
+
+
+def fp8_weight(rng, n, k, std=2.0 ** -6):
+    """A block-quantised FP8 weight as checkpoints hold it: N(0, std) values, each
+    128x128 block scaled by 2^ceil(log2(amax / 448)) and rounded to E4M3 (RNE).
+    Returns ([n, k] uint8 E4M3 codes, [ceil(n/128), ceil(k/128)] uint8 E8M0)."""
+    w = (rng.standard_normal((n, k)) * std).astype(np.float32)
+    nb, kb = (n + 127) // 128, (k + 127) // 128
+    pad = np.zeros((nb * 128, kb * 128), np.float32)
+    pad[:n, :k] = np.abs(w)
+    amax = pad.reshape(nb, 128, kb, 128).max(axis=(1, 3))
+    e = np.ceil(np.log2(np.maximum(amax, 1e-30) / 448.0)).astype(np.int32)
+    s = np.repeat(np.repeat(np.ldexp(np.float32(1), e), 128, 0)[:n], 128, 1)[:, :k].astype(np.float32)
+    codes = torch.from_numpy(w / s).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    return codes, (e + 127).astype(np.uint8)
+
+
+def shared_expert_weights(seed, hidden, inter):
+    """Shared expert in the checkpoint's FP8 form (numpy): w1/w3 [I, D] + [I/128, D/128],
+    w2 [D, I] + [D/128, I/128] (E4M3 codes, E8M0 128x128 block scales)."""
+    rng = np.random.default_rng(seed)
+    w1, w1s = fp8_weight(rng, inter, hidden)
+    w3, w3s = fp8_weight(rng, inter, hidden)
+    w2, w2s = fp8_weight(rng, hidden, inter)
+    return {"w1": w1, "w1s": w1s, "w2": w2, "w2s": w2s, "w3": w3, "w3s": w3s}
 
 
 def bf16_normal(rng, shape):

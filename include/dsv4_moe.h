@@ -178,6 +178,30 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
                            const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
                            float swiglu_limit, void* workspace, int64_t workspace_bytes, void* y, void* stream);
 
+/* The same layer with the shared expert folded in as one more group of the
+ * grouped GEMMs (bf16 profile): OffloadDeepseekV4MoE.forward's
+ * `out = self._routed(hs) + self.shared_experts(hs)` (deepseek_v4.py:262-264)
+ * with shared_experts = model_npu.py:469-489 Expert(mode="fp8"): the FP8
+ * round trip of x, E4M3 weights dequantised by 128x128 E8M0 block scales
+ * (npu_ops.py:161-167), SwiGLU with swiglu_limit and no routing weight, the
+ * FP8 round trip of h, and the down projection. The shared rows (flat indices
+ * T*K .. T*K+T-1) run in the same launches as the routed ones; y =
+ * bf16(bf16(routed sum) + shared row). sw1, sw3: E4M3 [I, D]; sw2: E4M3 [D, I];
+ * sw1s, sw3s: E8M0 [I, D/32]; sw2s: E8M0 [D, I/32], the block scales repeated
+ * per 32 along K (dsv4_expand_block_scales). */
+int dsv4_moe_layer_shared_workspace_bytes(int T, int K, int E, int D, int I, int64_t* bytes);
+int dsv4_moe_layer_forward_shared(const void* x, const void* topk_ids, int ids_int64, const float* topk_w, int T,
+                                  int K, int E, int D, int I, const void* expert_table, const void* sw1,
+                                  const void* sw1s, const void* sw3, const void* sw3s, const void* sw2,
+                                  const void* sw2s, float swiglu_limit, void* workspace, int64_t workspace_bytes,
+                                  void* y, void* stream);
+
+/* out[n][j] = block_scales[n / 128][j / 4] for n < n_rows, j < k/32: the
+ * 128x128 block scales of an FP8 weight [n_rows, k] (npu_ops.py:161-167,
+ * dequant_fp8_weight) repeated per 32 along K, the layout the grouped GEMMs
+ * read. block_scales: [ceil(n_rows/128), ceil(k/128)] E8M0; k % 32 == 0. */
+int dsv4_expand_block_scales(const void* block_scales, int64_t n_rows, int64_t k, void* out, void* stream);
+
 /* ------------------------------------------------------------------------
  * Expert slot cache (replaces ExpertBank's device caches, offload.py:22-151).
  * One device slot pool (caller-allocated, n_slots * record_bytes, 256-byte

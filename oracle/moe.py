@@ -10,6 +10,9 @@
   per-expert ``_expert`` loop), the reference's own parity baseline.
 * ``grouped_gemm`` - ``npu_grouped_matmul(x=[x], weight=[w_g^T...],
   group_list_type=1)``: per-group ``x_g @ W_g^T`` (``_bench_gmm.py:8-22``).
+* ``shared_expert_bf16`` - ``model_npu.py:469-489`` (the FP8 shared expert),
+  and ``routed_plus_shared_bf16`` - ``deepseek_v4.py:262-264`` (routed output
+  plus shared output, bf16 + bf16).
 
 GEMM products are accumulated in float64 and rounded once to fp32 then bf16;
 the reference accumulates in fp32 on the NPU, so GEMM outputs are compared
@@ -190,3 +193,29 @@ def dequant_gemv(x_bf16, w_packed, scale):
     """Config-0 check: bf16 ``x @ dequant(W)^T`` -> bf16 bits."""
     wf = Q.dequant_fp4_weight_f32(w_packed, scale)
     return Q.f32_to_bf16_bits(matmul_nt(Q.bf16_bits_to_f32(x_bf16), wf))
+
+
+def shared_expert_bf16(x_bf16, sh, swiglu_limit=10.0):
+    """``model_npu.py:469-489`` Expert(mode="fp8"): every Linear takes the FP8
+    round trip of its input (``:114-117``) and the weight dequantised to bf16
+    (``npu_ops.py:161-167``); SwiGLU with the clamp and no routing weight.
+    ``sh`` holds ``w{1,2,3}`` E4M3 codes and ``w{1,2,3}s`` 128x128 block
+    scales. Returns bf16 bits [T, D]."""
+    x_bf16 = np.asarray(x_bf16, np.uint16)
+    w1 = Q.dequant_fp8_weight_f32(sh["w1"], sh["w1s"])
+    w3 = Q.dequant_fp8_weight_f32(sh["w3"], sh["w3s"])
+    w2 = Q.dequant_fp8_weight_f32(sh["w2"], sh["w2s"])
+    xq = Q.bf16_bits_to_f32(Q.act_quant(x_bf16, 128)[0])                 # :115
+    gate = Q.f32_to_bf16_f32(matmul_nt(xq, w1))                          # :479
+    up = Q.f32_to_bf16_f32(matmul_nt(xq, w3))                            # :480
+    h = swiglu(gate, up, np.ones(xq.shape[0], np.float32), swiglu_limit)  # :481-486 (x 1.0 is exact)
+    hq = Q.bf16_bits_to_f32(Q.act_quant(Q.f32_to_bf16_bits(h), 128)[0])  # :489 -> :115
+    return Q.f32_to_bf16_bits(matmul_nt(hq, w2))
+
+
+def routed_plus_shared_bf16(x_bf16, topk_ids, topk_w, experts, sh, n_experts=256, swiglu_limit=10.0):
+    """``deepseek_v4.py:262-264``: ``out = self._routed(hs) + self.shared_experts(hs)``,
+    a bf16 + bf16 addition (rounded once, from the exact fp32 sum)."""
+    yr = routed_bf16(x_bf16, topk_ids, topk_w, experts, n_experts=n_experts, swiglu_limit=swiglu_limit)["y"]
+    ys = shared_expert_bf16(x_bf16, sh, swiglu_limit)
+    return Q.f32_to_bf16_bits(Q.bf16_bits_to_f32(yr) + Q.bf16_bits_to_f32(ys)), yr, ys

@@ -263,3 +263,17 @@ def dequant_fp4_weight(w_packed, scale):
 def fp4_codes_to_f32(packed, scale, block=32):
     """Dequantise MXFP4 activations/weights (same math as the weight dequant)."""
     return dequant_fp4_weight_f32(packed, scale)
+
+
+def dequant_fp8_weight_f32(codes, scale, block=128):
+    """``npu_ops.py:161-167`` dequant_fp8_weight before its bf16 cast: E4M3 code
+    value times ``2^(s-127)`` of its 128x128 block. ``codes`` [N, K] uint8,
+    ``scale`` [ceil(N/128), ceil(K/128)] uint8. Exact in bf16 for the scale
+    range of the checkpoints (a 4-bit significand times a power of two)."""
+    c = np.asarray(codes, np.uint8)
+    N, K = c.shape
+    v = e4m3fn_code_to_f32(c)
+    s = e8m0_to_fp32(np.asarray(scale, np.uint8))
+    s = np.repeat(np.repeat(s, block, axis=0)[:N], block, axis=1)[:, :K]
+    with np.errstate(invalid="ignore", over="ignore"):
+        return (v * s).astype(np.float32)

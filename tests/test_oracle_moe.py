@@ -169,3 +169,61 @@ def test_lru_known_answer_sequence():
     zero.access((0, 0))
     zero.access((0, 0))
     assert len(zero.cache) == 0 and zero.stats()["misses"] == 2
+
+
+def test_fp8_weight_dequant_matches_torch_float8():
+    # npu_ops.py:161-167: E4M3 code value (torch's own float8_e4m3fn decode) x 2^(s-127)
+    # per 128x128 block, exact in bf16
+    rng = np.random.default_rng(3)
+    codes, sc = synth.fp8_weight(rng, 200, 384)
+    got = Q.dequant_fp8_weight_f32(codes, sc)
+    vals = torch.from_numpy(codes).view(torch.float8_e4m3fn).float()
+    s = torch.pow(2.0, torch.from_numpy(sc.astype(np.float32)) - 127.0)
+    s = s.repeat_interleave(128, 0)[:200].repeat_interleave(128, 1)[:, :384]
+    want = (vals * s).numpy()
+    assert np.array_equal(got, want)
+    assert np.array_equal(Q.f32_to_bf16_f32(got), got)            # bf16-exact
+    assert not np.isnan(got).any() and 0x7F not in codes and 0xFF not in codes
+    # each block's largest magnitude sits in the top binade of E4M3 (256..448)
+    a = np.abs(vals.numpy())
+    top = np.array([[a[i:i + 128, j:j + 128].max() for j in range(0, 384, 128)] for i in range(0, 200, 128)])
+    assert np.all((top >= 224) & (top <= 448))
+
+
+def _e2m1_as_fp8(mx, n, k):
+    """An MXFP4 weight whose per-32 scales are constant over 128x128 blocks, as
+    E4M3 codes + block scales holding exactly the same values."""
+    vals = Q.dequant_fp4_weight_f32(mx[0], np.full((n, k // 32), 127, np.uint8))  # E2M1 values, scale 1
+    code = {v: c for c in range(256) if c not in (0x7F, 0xFF)
+            for v in [float(Q.e4m3fn_code_to_f32(np.array([c], np.uint8))[0])]}
+    codes = np.vectorize(lambda v: code[float(v)])(vals).astype(np.uint8)
+    return codes, mx[1][::128, ::4].copy()
+
+
+def test_shared_expert_equals_a_routed_expert_with_weight_one():
+    # model_npu.Expert (FP8 weights, no routing weight) and the routed path are the
+    # same computation: for weights both formats hold exactly, the shared expert's
+    # output equals the routed path with K = 1 and weight 1.0 bit for bit
+    T, D, I = 6, 256, 256
+    rng = np.random.default_rng(8)
+    ex, sh = {}, {}
+    for w, (n, k) in (("w1", (I, D)), ("w3", (I, D)), ("w2", (D, I))):
+        p = rng.integers(0, 256, size=(n, k // 2), dtype=np.uint8)
+        blk = rng.integers(117, 124, size=(n // 128, k // 128), dtype=np.uint8)
+        s32 = np.repeat(np.repeat(blk, 128, 0), 4, 1)
+        ex[w + "p"], ex[w + "s"] = p, s32
+        sh[w], sh[w + "s"] = _e2m1_as_fp8((p, s32), n, k)
+        assert np.array_equal(Q.dequant_fp8_weight_f32(sh[w], sh[w + "s"]), Q.dequant_fp4_weight_f32(p, s32))
+    x = synth.bf16_normal(np.random.default_rng(9), (T, D)).view(torch.int16).numpy().view(np.uint16)
+    ys = M.shared_expert_bf16(x, sh)
+    yr = M.routed_bf16(x, np.zeros((T, 1), np.int64), np.ones((T, 1), np.float32), {0: ex}, n_experts=1)["y"]
+    assert np.array_equal(ys, yr)
+    # the layer output adds the two bf16 tensors (deepseek_v4.py:262-264)
+    ids = synth.zipf_topk(T, 2, 4, synth.rank_permutation(4), np.random.default_rng(1))
+    w = synth.routing_weights(T, 2, 2)
+    exs = {e: synth.expert_weights(e, D, I) for e in range(4)}
+    y, y_r, y_s = M.routed_plus_shared_bf16(x, ids, w, exs, sh, n_experts=4)
+    assert np.array_equal(y_s, ys)
+    want = (torch.from_numpy(y_r.view(np.int16)).view(torch.bfloat16)
+            + torch.from_numpy(y_s.view(np.int16)).view(torch.bfloat16))
+    assert np.array_equal(y, want.view(torch.int16).numpy().view(np.uint16))
