@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default="",
-                    help="profile helper: run only 'decode', 'dequant', 'prefill', 'router' or 'offload'")
+                    help="profile helper: run only 'decode', 'dequant', 'prefill', 'router', 'shared' or 'offload'")
     ap.add_argument("--offload-steps", type=int, default=512, help="decode steps of the expert-offload leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy 1 GiB device-to-device (a plain copy of known size for counter calibration)")
@@ -91,17 +91,21 @@ def routing_batches(n, T, K, seed):
     return out
 
 
-def time_layer(runner, batches_dev, tables, steps, warmup, profile, rule):
+def time_layer(runner, batches_dev, tables, steps, warmup, profile, rule, shared=None):
+    """Seconds per layer call; ``shared`` (a list of prepared shared experts, one
+    per weight set) runs the layer with the shared expert fused in."""
     n = len(batches_dev)
     L = len(tables)
     for i in range(warmup):
         x, ids, w = batches_dev[i % n]
-        runner.forward(x, ids, w, tables[i % L], profile=profile, rule=rule)
+        runner.forward(x, ids, w, tables[i % L], profile=profile, rule=rule,
+                       shared=shared[i % L] if shared else None)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         x, ids, w = batches_dev[i % n]
-        runner.forward(x, ids, w, tables[i % L], profile=profile, rule=rule)
+        runner.forward(x, ids, w, tables[i % L], profile=profile, rule=rule,
+                       shared=shared[i % L] if shared else None)
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) / steps
 
@@ -272,6 +276,32 @@ def measure_offload(dev, n_steps=512, n_layers=8, n_slots=512, T=8, K=8, warmup_
     return res
 
 
+def measure_shared(dev, gen, steps=200, n_sets=8):
+    """The decode layer (8 tokens, top-8 of 256, hidden 4096, inter 2048, bf16
+    profile) with the FP8 shared expert (inter 2048, 128x128 block scales) fused
+    into its launches, against the routed-only layer on the same inputs. Each of
+    the n_sets weight sets has its own shared expert (25 MB of E4M3 weights)."""
+    from dsv4_hip import ops, PROFILE_BF16, RULE_OCP_FLOOR, synth
+    pools, tables = gen_layer_weights(dev, n_sets, gen)
+    shared = []
+    for i in range(n_sets):
+        sh = synth.shared_expert_weights(900 + i, D, I)
+        d = {k: torch.from_numpy(v).to(dev) for k, v in sh.items()}
+        shared.append(ops.prepare_shared_expert(d["w1"], d["w1s"], d["w3"], d["w3s"], d["w2"], d["w2s"]))
+    host = routing_batches(64, 8, 8, 11)
+    dev_b = [(x.to(dev), torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(dev)) for x, ids, w in host]
+    runner = ops.LayerRunner(dev, E, D, I)
+    t_r = time_layer(runner, dev_b, tables, steps, 20, PROFILE_BF16, RULE_OCP_FLOOR)
+    t_s = time_layer(runner, dev_b, tables, steps, 20, PROFILE_BF16, RULE_OCP_FLOOR, shared=shared)
+    shared_bytes = 3 * D * I + 3 * D * I // 32
+    del pools, tables, shared
+    torch.cuda.empty_cache()
+    return {"ms_per_layer_routed": t_r * 1e3, "ms_per_layer_routed_plus_shared": t_s * 1e3,
+            "tokens_per_s_with_shared": 8 / t_s, "shared_extra_us": (t_s - t_r) * 1e6,
+            "shared_weight_bytes": shared_bytes,
+            "shared_extra_gbs": shared_bytes / max(t_s - t_r, 1e-9) / 1e9}
+
+
 def measure_router(dev, iters=200):
     """dsv4_moe_route (gate logits + score + top-8 + weights) at decode and prefill
     token counts: 256 experts, hidden 4096, fp32 gate weight, sqrt(softplus) scores
@@ -408,6 +438,8 @@ def main():
         torch.cuda.empty_cache()
     if not args.no_extra and args.only in ("", "router"):
         extra["router"] = measure_router(dev)
+    if not args.no_extra and args.only in ("", "shared"):
+        extra["decode_with_shared_expert"] = measure_shared(dev, gen)
     if not args.no_extra and args.only in ("", "offload") and args.offload_steps > 0:
         extra["offload_config4"] = measure_offload(dev, n_steps=args.offload_steps)
     if extra:

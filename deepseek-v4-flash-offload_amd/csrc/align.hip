@@ -48,9 +48,11 @@ __device__ int block_exclusive_scan(int v, int* lds_waves, int* out_total) {
   return r;
 }
 
-// n_shared > 0 appends the shared expert as one more group after the routed
-// experts: n_shared rows with flat indices R .. R+n_shared-1, block_expert = E.
-// The padding sentinel is then R + n_shared.
+// n_shared > 0 adds the shared expert as one more group, placed first: n_shared
+// rows with flat indices R .. R+n_shared-1 and block_expert = E in the leading
+// blocks (its workgroups stream twice the bytes of a routed one, so they are
+// dispatched first rather than left as the launch's tail). The routed experts
+// follow; the padding sentinel is R + n_shared.
 template <typename IdT, int NT>
 __device__ void align_body(const IdT* __restrict__ ids, const float* __restrict__ topk_w, int R, int K, int E,
                            int block_m, int max_blocks, const Dsv4AlignOut& o, int n_shared = 0) {
@@ -83,8 +85,9 @@ __device__ void align_body(const IdT* __restrict__ ids, const float* __restrict_
   // 2. scans over experts (E <= kThreads)
   const int c = (tid < E) ? cnt[tid] : 0;
   const int padded = ((c + block_m - 1) / block_m) * block_m;
+  const int shared_padded = ((n_shared + block_m - 1) / block_m) * block_m;
   const int ou = block_exclusive_scan<NT>(c, scan_tmp, &totals[0]);
-  const int op = block_exclusive_scan<NT>(padded, scan_tmp, &totals[1]);
+  const int op = block_exclusive_scan<NT>(padded, scan_tmp, &totals[1]) + shared_padded;
   const int oa = block_exclusive_scan<NT>(c > 0 ? 1 : 0, scan_tmp, &totals[2]);
   if (tid < E) {
     off_u[tid] = ou;
@@ -95,7 +98,6 @@ __device__ void align_body(const IdT* __restrict__ ids, const float* __restrict_
   }
   __syncthreads();
   const int pad_id = R + n_shared;  // padding sentinel
-  const int shared_padded = ((n_shared + block_m - 1) / block_m) * block_m;
   const int total_padded = totals[1] + shared_padded;
   const int total_blocks = total_padded / block_m;
   const int cap = max_blocks * block_m;
@@ -106,9 +108,9 @@ __device__ void align_body(const IdT* __restrict__ ids, const float* __restrict_
     const int p1 = min(op + padded, cap);
     for (int p = op + c; p < p1; ++p) o.sorted_ids[p] = pad_id;
   }
-  // the shared expert's group: rows R + i in order, after every routed expert
+  // the shared expert's group: rows R + i in order, ahead of the routed experts
   for (int i = tid; i < shared_padded; i += kThreads) {
-    const int p = totals[1] + i;
+    const int p = i;
     if (p < cap) {
       o.sorted_ids[p] = i < n_shared ? R + i : pad_id;
       if (i % block_m == 0) o.block_expert[p / block_m] = E;

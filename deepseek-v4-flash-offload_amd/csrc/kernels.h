@@ -41,8 +41,8 @@ hipError_t launch_moe_align(const void* topk_ids, int ids_int64, const float* to
 
 // align (workgroup 0) and activation quantisation (workgroups 1..) in one launch;
 // qfmt 0 = FP8 per-128 codes + E8M0 x4 scales, 1 = MXFP4 per-32 (rule 0/1).
-// n_shared > 0 appends a group of n_shared rows (flat indices R..) with
-// block_expert E after the routed experts; the padding sentinel becomes R + n_shared.
+// n_shared > 0 adds a group of n_shared rows (flat indices R..) with
+// block_expert E ahead of the routed experts; the padding sentinel becomes R + n_shared.
 hipError_t launch_moe_align_quant(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K, int E,
                                   int block_m, int max_blocks, const Dsv4AlignOut& o, const uint16_t* x,
                                   int64_t n_elems, int qfmt, int rule, void* q_codes, void* q_scale,

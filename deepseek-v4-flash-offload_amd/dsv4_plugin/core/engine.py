@@ -5,7 +5,9 @@ Surface of ``dsv4_plugin/core/engine.py`` in the reference (``:23-116``):
 ``capture`` / ``get`` / ``get_packed`` / ``stats`` and the process-wide
 ``get_engine`` singleton (``DSV4_EXPERT_SLOTS``, default 512). Captured experts
 go into an ``offload.ExpertBank`` whose packed slots feed the HIP grouped GEMMs;
-``acquire_table`` is the batched fast path the MoE layer uses.
+``acquire_table`` is the batched fast path the MoE layer uses. The shared
+expert's FP8 tensors are copied on the side (``capture_shared``) so the layer
+can run it inside the routed launches (``get_shared``).
 """
 
 import os
@@ -26,6 +28,10 @@ _KEY = re.compile(r"(?:^|\.)(?P<blk>layers|mtp)\.(?P<idx>\d+)\.ffn\.experts\.(?P
                   r"\.(?P<w>w[123])\.(?P<kind>weight|scale)$")
 _PART = {"weight": "p", "scale": "s"}
 _PARTS = ("w1p", "w1s", "w2p", "w2s", "w3p", "w3s")
+# The shared expert of layer L in the checkpoint's FP8 form:
+# [model.]layers.<L>.ffn.shared_experts.w{1,2,3}.{weight,scale}
+_SHARED_KEY = re.compile(r"(?:^|\.)layers\.(?P<idx>\d+)\.ffn\.shared_experts\.(?P<w>w[123])"
+                         r"\.(?P<kind>weight|scale)$")
 
 
 def parse_expert_name(name: str):
@@ -36,6 +42,14 @@ def parse_expert_name(name: str):
     idx = int(m.group("idx"))
     layer = idx if m.group("blk") == "layers" else -1 - idx
     return layer, int(m.group("eid")), m.group("w"), m.group("kind")
+
+
+def parse_shared_name(name: str):
+    """``(layer, "w1"|"w2"|"w3", "weight"|"scale")`` of a shared-expert key, or None."""
+    m = _SHARED_KEY.search(name)
+    if m is None:
+        return None
+    return int(m.group("idx")), m.group("w"), m.group("kind")
 
 
 def is_expert_weight(name: str, include_mtp: bool = False) -> bool:
@@ -51,6 +65,35 @@ class ExpertOffloadEngine:
         self.bank = ExpertBank(capacity=slot_capacity, device=device, dtype=dtype)
         self._pending = {}   # (layer, eid) -> {part: tensor} until all six parts arrive
         self.captured = 0
+        self._shared = {}    # layer -> {"w1": codes, "w1s": block scales, ...} (host copies)
+        self._shared_dev = {}
+
+    def capture_shared(self, name: str, tensor: torch.Tensor) -> bool:
+        """Keep a host copy of a shared-expert FP8 tensor (the weight stream still
+        delivers it to its own module); True if ``name`` is one."""
+        parsed = parse_shared_name(name)
+        if parsed is None:
+            return False
+        layer, w, kind = parsed
+        self._shared.setdefault(layer, {})[w + ("s" if kind == "scale" else "")] = tensor.detach().to("cpu")
+        self._shared_dev.pop(layer, None)
+        return True
+
+    def get_shared(self, layer: int, device):
+        """The shared expert of ``layer`` prepared for the fused layer launch
+        (``dsv4_hip.ops.prepare_shared_expert``), or None until all six tensors
+        were captured."""
+        parts = self._shared.get(int(layer))
+        if parts is None or len(parts) < 6:
+            return None
+        key = (int(layer), str(device))
+        prep = self._shared_dev.get(key)
+        if prep is None:
+            from dsv4_hip import ops
+            d = {k: v.to(device) for k, v in parts.items()}
+            prep = ops.prepare_shared_expert(d["w1"], d["w1s"], d["w3"], d["w3s"], d["w2"], d["w2s"])
+            self._shared_dev[key] = prep
+        return prep
 
     def capture(self, name: str, tensor: torch.Tensor) -> bool:
         """Take an expert tensor from the weight stream; True if consumed."""

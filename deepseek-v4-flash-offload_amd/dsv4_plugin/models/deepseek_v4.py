@@ -54,6 +54,12 @@ _MXFP4_GMM = os.environ.get("DSV4_MXFP4_GMM", "0") == "1"
 _MX_RULE = os.environ.get("DSV4_MX_RULE", "ocp_floor")
 _RULES = {"ocp_floor": _lib.RULE_OCP_FLOOR, "ceil_div6": _lib.RULE_CEIL_DIV6}
 
+# Shared expert inside the routed launches (bf16 profile): when the engine
+# captured the layer's FP8 shared-expert tensors from the weight stream, forward
+# runs them as one more group of the grouped GEMMs instead of calling the
+# shared MLP. Read at call time; env DSV4_FUSE_SHARED=1.
+_FUSE_SHARED = os.environ.get("DSV4_FUSE_SHARED", "0") == "1"
+
 # Predictive prefetch: layer L routes its input with layer L+1's gate (or reads
 # layer L+1's tid2eid rows on hash layers, which is exact) and starts the copies
 # of the experts that picks, after its own slots are acquired and before its
@@ -216,7 +222,7 @@ class OffloadDeepseekV4MoE(_BASE):
         ids = np.unique(ids[(ids >= 0) & (ids < nxt.n_routed_experts)])
         return eng.prefetch(nxt.layer_idx, ids) if ids.size else 0
 
-    def _run_experts(self, hs, weights, indices, profile, input_ids=None):
+    def _run_experts(self, hs, weights, indices, profile, input_ids=None, shared=None):
         T, D = hs.shape
         x = hs if (hs.dtype == torch.bfloat16 and hs.is_contiguous()) else hs.to(torch.bfloat16).contiguous()
         if T == 0:
@@ -226,15 +232,22 @@ class OffloadDeepseekV4MoE(_BASE):
             self._prefetch_next(hs, input_ids)
         limit = self.swiglu_limit if (self.swiglu_limit and self.swiglu_limit > 0) else 0.0
         y = _runner(hs.device, self.n_routed_experts, D, inter).forward(
-            x, indices, weights, table, profile=profile, rule=_RULES[_MX_RULE], swiglu_limit=limit)
+            x, indices, weights, table, profile=profile, rule=_RULES[_MX_RULE], swiglu_limit=limit, shared=shared)
         return y.type_as(hs)
 
-    def _routed(self, hs: torch.Tensor, input_ids=None) -> torch.Tensor:
+    def _routed(self, hs: torch.Tensor, input_ids=None, shared=None) -> torch.Tensor:
         """Routed-expert output ``[T, D]`` (``deepseek_v4.py:150-197``); the a4w4
-        profile when the module toggle ``_MXFP4_GMM`` is set (``:199-245``)."""
+        profile when the module toggle ``_MXFP4_GMM`` is set (``:199-245``).
+        ``shared`` (a prepared FP8 shared expert, bf16 profile) adds the shared
+        expert's output computed in the same launches."""
         weights, indices = self._route(hs, input_ids)
         profile = _lib.PROFILE_A4W4 if _MXFP4_GMM else _lib.PROFILE_BF16
-        return self._run_experts(hs, weights, indices, profile, input_ids)
+        return self._run_experts(hs, weights, indices, profile, input_ids, shared)
+
+    def _fused_shared(self, hs):
+        if not (_FUSE_SHARED and not _MXFP4_GMM and hs.is_cuda and hasattr(self.engine, "get_shared")):
+            return None
+        return self.engine.get_shared(self.layer_idx, hs.device)
 
     def _routed_mxfp4(self, s_w, row, active, group_list, T, hs):
         """a4w4 path from the reference's sorted view (``deepseek_v4.py:199``
@@ -255,9 +268,13 @@ class OffloadDeepseekV4MoE(_BASE):
             hs = v4.sequence_parallel_chunk(hs)
             if input_ids is not None:
                 input_ids = v4.sequence_parallel_chunk(input_ids)
-        out = self._routed(hs, input_ids)
-        if self.shared_experts is not None:
-            out = out + self.shared_experts(hs)
+        shared = self._fused_shared(hs)
+        if shared is not None:
+            out = self._routed(hs, input_ids, shared=shared)
+        else:
+            out = self._routed(hs, input_ids)
+            if self.shared_experts is not None:
+                out = out + self.shared_experts(hs)
         if self.is_sequence_parallel:
             out = v4.tensor_model_parallel_all_gather(out, 0)[:num_tokens]
         return out.view(num_tokens, hidden_dim)
@@ -275,6 +292,8 @@ def _offload_load_weights(self, weights):
             if is_expert_weight(name):
                 engine.capture(name, w)
             else:
+                if hasattr(engine, "capture_shared"):
+                    engine.capture_shared(name, w)   # a copy; the shared MLP still loads it
                 yield name, w
 
     return _ORIG_LOAD_WEIGHTS(self, filtered())

@@ -375,3 +375,36 @@ def test_prefetch_next_layer(gpu, monkeypatch, n_slots, next_hash):
         ref = M.routed_bf16(xb, idx.cpu().numpy(), w.cpu().numpy(), {e: host[layer, e] for e in range(E)},
                             n_experts=E)
         assert rel(Q.bf16_bits_to_f32(_bits(y)), Q.bf16_bits_to_f32(ref["y"])) <= 1e-2, layer
+
+
+def test_forward_fuses_the_captured_shared_expert(gpu, monkeypatch):
+    # the weight stream's shared-expert tensors (captured on the side) run inside the
+    # routed launches; forward = routed + shared (deepseek_v4.py:262-264)
+    E, K, D, I, T, layer = 32, 6, 1024, 512, 8, 3
+    engine = ExpertOffloadEngine(slot_capacity=16, device="cuda:0")
+    host = {}
+    for e in range(E):
+        host[e] = synth.expert_weights(e, D, I)
+        for w in ("w1", "w2", "w3"):
+            engine.capture(f"layers.{layer}.ffn.experts.{e}.{w}.weight", torch.from_numpy(host[e][w + "p"]).view(torch.int8))
+            engine.capture(f"layers.{layer}.ffn.experts.{e}.{w}.scale",
+                           torch.from_numpy(host[e][w + "s"]).view(torch.float8_e8m0fnu))
+    sh = synth.shared_expert_weights(77, D, I)
+    for w in ("w1", "w2", "w3"):
+        assert engine.capture_shared(f"model.layers.{layer}.ffn.shared_experts.{w}.weight",
+                                     torch.from_numpy(sh[w]).view(torch.float8_e4m3fn))
+        assert engine.capture_shared(f"model.layers.{layer}.ffn.shared_experts.{w}.scale",
+                                     torch.from_numpy(sh[w + "s"]).view(torch.float8_e8m0fnu))
+    m = _make_plugin(engine, E, K, layer, False, D)
+    x = (synth.bf16_normal(np.random.default_rng(5), (T, D)).float() * 0.5).to(torch.bfloat16).to(gpu)
+    w, idx = m._route(x, None)
+    xb = _bits(x)
+    want, want_r, _ = M.routed_plus_shared_bf16(xb, idx.cpu().numpy(), w.cpu().numpy(), host, sh, n_experts=E)
+    monkeypatch.setattr(mod, "_FUSE_SHARED", False)
+    y_r = m.forward(x)                          # shared_experts is None: routed only
+    monkeypatch.setattr(mod, "_FUSE_SHARED", True)
+    y = m.forward(x)
+    torch.cuda.synchronize()
+    assert rel(Q.bf16_bits_to_f32(_bits(y_r)), Q.bf16_bits_to_f32(want_r)) <= 1e-2
+    assert rel(Q.bf16_bits_to_f32(_bits(y)), Q.bf16_bits_to_f32(want)) <= 1e-2
+    assert engine.get_shared(layer, gpu) is engine.get_shared(layer, gpu)   # prepared once per device

@@ -159,3 +159,34 @@ def test_moe_module_constructs_without_vllm(monkeypatch):
     ref_w = scores.gather(1, idx)
     ref_w = ref_w / ref_w.sum(-1, keepdim=True) * 1.5
     assert torch.allclose(w, ref_w)
+
+
+def test_tee_keeps_a_copy_of_the_shared_expert():
+    # shared-expert keys still reach the wrapped loader (its shared MLP loads them);
+    # the engine keeps a host copy per layer for the fused launch
+    from dsv4_plugin.core.engine import parse_shared_name
+    assert parse_shared_name("model.layers.7.ffn.shared_experts.w2.scale") == (7, "w2", "scale")
+    assert parse_shared_name("layers.7.ffn.experts.3.w2.scale") is None
+    assert parse_shared_name("mtp.0.ffn.shared_experts.w1.weight") is None
+    engine = ExpertOffloadEngine(slot_capacity=4, device="cpu")
+    saved_engine, eng._ENGINE = eng._ENGINE, engine
+    received = []
+
+    def stub_original(self, weights):
+        received.extend(name for name, _ in weights)
+
+    names = [f"model.layers.{l}.ffn.shared_experts.{w}.{k}" for l in (1, 2) for w in ("w1", "w2", "w3")
+             for k in ("weight", "scale")]
+    names += ["model.layers.1.attn.wq.weight", "model.layers.1.ffn.experts.0.w1.weight"]
+    saved = mod._ORIG_LOAD_WEIGHTS
+    mod._ORIG_LOAD_WEIGHTS = stub_original
+    try:
+        mod._offload_load_weights(object(), ((n, torch.full((2, 2), i, dtype=torch.uint8))
+                                             for i, n in enumerate(names)))
+    finally:
+        mod._ORIG_LOAD_WEIGHTS = saved
+        eng._ENGINE = saved_engine
+    assert received == [n for n in names if ".ffn.experts." not in n]
+    assert sorted(engine._shared) == [1, 2] and sorted(engine._shared[1]) == ["w1", "w1s", "w2", "w2s", "w3", "w3s"]
+    assert int(engine._shared[2]["w3s"][0, 0]) == names.index("model.layers.2.ffn.shared_experts.w3.scale")
+    assert engine.get_shared(5, "cpu") is None      # nothing captured for layer 5
