@@ -74,9 +74,10 @@ __device__ void align_body(const IdT* __restrict__ ids, const float* __restrict_
   if (tid == 0) bad = 0;
   __syncthreads();
 
-  // 1. histogram
+  // 1. histogram (the first chunk's ids stay in registers for the scatter)
+  const long long id0 = tid < R ? (long long)ids[tid] : 0;
   for (int i = tid; i < R; i += kThreads) {
-    long long e = (long long)ids[i];
+    long long e = i == tid ? id0 : (long long)ids[i];
     if (e < 0 || e >= E) { atomicAdd(&bad, 1); continue; }
     atomicAdd(&cnt[(int)e], 1);
   }
@@ -132,7 +133,7 @@ __device__ void align_body(const IdT* __restrict__ ids, const float* __restrict_
     const int i = base + tid;
     int e = E;
     if (i < R) {
-      long long ee = (long long)ids[i];
+      long long ee = base == 0 ? id0 : (long long)ids[i];
       if (ee >= 0 && ee < E) e = (int)ee;
     }
     unsigned long long peers = __ballot(1);

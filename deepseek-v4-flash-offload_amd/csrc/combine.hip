@@ -77,14 +77,26 @@ __global__ __launch_bounds__(64) void combine_flat_kernel(const u32x4* __restric
   const int lane = threadIdx.x;
   const long long key = lane < K ? (long long)ids[(int64_t)t * K + lane] : 0;
   const int rank = wave_rank(key, K);
+  // lane r receives the k of rank r (the inverse permutation, pushed by ds_permute)
+  const int k_of_rank = __builtin_amdgcn_ds_permute((lane < K ? rank : lane) * 4, lane);
   const int vecs = D / 8;
   const int c = blockIdx.x * 64 + lane;
+  const bool live = c < vecs;
+  const u32x4* srow = src + (int64_t)t * K * vecs + (live ? c : 0);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int r = 0; r < K; ++r) {
-    const int k = wave_select_rank(rank, K, r);
-    if (c < vecs) accumulate8(acc, src[((int64_t)t * K + k) * vecs + c]);
+  // 8 rows' loads in flight at once, then summed in rank order
+  for (int r0 = 0; r0 < K; r0 += 8) {
+    u32x4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int k = __shfl(k_of_rank, min(r0 + i, K - 1), 64);
+      v[i] = (r0 + i < K) ? srow[(int64_t)k * vecs] : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (r0 + i < K) accumulate8(acc, v[i]);
   }
-  if (c >= vecs) return;
+  if (!live) return;
   if (shared_rows) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = dsv4::bf16_to_f32(dsv4::f32_to_bf16(acc[i]));
