@@ -48,43 +48,24 @@ __device__ int block_exclusive_scan(int v, int* lds_waves, int* out_total) {
   return r;
 }
 
-// n_shared > 0 adds the shared expert as one more group, placed first: n_shared
-// rows with flat indices R .. R+n_shared-1 and block_expert = E in the leading
-// blocks (its workgroups stream twice the bytes of a routed one, so they are
-// dispatched first rather than left as the launch's tail). The routed experts
-// follow; the padding sentinel is R + n_shared.
-template <typename IdT, int NT>
-__device__ void align_body(const IdT* __restrict__ ids, const float* __restrict__ topk_w, int R, int K, int E,
-                           int block_m, int max_blocks, const Dsv4AlignOut& o, int n_shared = 0) {
-  constexpr int kThreads = NT;
+// Padded layout from the per-expert counts (thread e < E holds count c of
+// expert e; bad = out-of-range ids): unpadded and padded offsets, active ranks,
+// block_expert, the padding sentinel, num_post_padded, the optional per-expert
+// outputs, and off_u/off_p (LDS) for the scatter. n_shared > 0 adds the shared
+// expert as one more group, placed first: n_shared rows with flat indices
+// R .. R+n_shared-1 and block_expert = E in the leading blocks (its
+// workgroups stream twice the bytes of a routed one, so they are dispatched
+// first rather than left as the launch's tail). The routed experts follow;
+// the padding sentinel is R + n_shared.
+// write = false: only off_u/off_p (for workgroups that recompute the layout
+// to scatter their own entries).
+template <int NT>
+__device__ void align_layout(int c, int bad, int R, int E, int block_m, int max_blocks, int n_shared,
+                             const Dsv4AlignOut& o, int* off_u, int* off_p, bool write = true) {
   constexpr int kWaves = NT / 64;
-  extern __shared__ int lds[];
-  int* cnt = lds;                    // [E + 1] (slot E collects out-of-range ids)
-  int* off_u = cnt + (E + 1);        // [E]
-  int* off_p = off_u + E;            // [E]
-  int* running = off_p + E;          // [E + 1]
-  int* wcount = running + (E + 1);   // [kWaves][E + 1]
   __shared__ int scan_tmp[kWaves];
   __shared__ int totals[3];
-  __shared__ int bad;
-
   const int tid = threadIdx.x;
-  for (int i = tid; i < E + 1; i += kThreads) { cnt[i] = 0; running[i] = 0; }
-  for (int i = tid; i < kWaves * (E + 1); i += kThreads) wcount[i] = 0;
-  if (tid == 0) bad = 0;
-  __syncthreads();
-
-  // 1. histogram (the first chunk's ids stay in registers for the scatter)
-  const long long id0 = tid < R ? (long long)ids[tid] : 0;
-  for (int i = tid; i < R; i += kThreads) {
-    long long e = i == tid ? id0 : (long long)ids[i];
-    if (e < 0 || e >= E) { atomicAdd(&bad, 1); continue; }
-    atomicAdd(&cnt[(int)e], 1);
-  }
-  __syncthreads();
-
-  // 2. scans over experts (E <= kThreads)
-  const int c = (tid < E) ? cnt[tid] : 0;
   const int padded = ((c + block_m - 1) / block_m) * block_m;
   const int shared_padded = ((n_shared + block_m - 1) / block_m) * block_m;
   const int ou = block_exclusive_scan<NT>(c, scan_tmp, &totals[0]);
@@ -93,6 +74,12 @@ __device__ void align_body(const IdT* __restrict__ ids, const float* __restrict_
   if (tid < E) {
     off_u[tid] = ou;
     off_p[tid] = op;
+  }
+  if (!write) {
+    __syncthreads();
+    return;
+  }
+  if (tid < E) {
     if (o.counts) o.counts[tid] = c;
     if (o.expert_start) o.expert_start[tid] = op;
     if (o.active) o.active[tid] = -1;
@@ -110,11 +97,10 @@ __device__ void align_body(const IdT* __restrict__ ids, const float* __restrict_
     for (int p = op + c; p < p1; ++p) o.sorted_ids[p] = pad_id;
   }
   // the shared expert's group: rows R + i in order, ahead of the routed experts
-  for (int i = tid; i < shared_padded; i += kThreads) {
-    const int p = i;
-    if (p < cap) {
-      o.sorted_ids[p] = i < n_shared ? R + i : pad_id;
-      if (i % block_m == 0) o.block_expert[p / block_m] = E;
+  for (int i = tid; i < shared_padded; i += NT) {
+    if (i < cap) {
+      o.sorted_ids[i] = i < n_shared ? R + i : pad_id;
+      if (i % block_m == 0) o.block_expert[i / block_m] = E;
     }
   }
   if (tid == 0) {
@@ -123,17 +109,29 @@ __device__ void align_body(const IdT* __restrict__ ids, const float* __restrict_
     if (o.status) o.status[0] = bad + (total_blocks > max_blocks ? (1 << 30) : 0);
   }
   __syncthreads();
+}
 
-  // 3. stable scatter
-  const int lane = tid & 63, wave = tid >> 6;
+// Stable scatter of entries [i0, i1): in chunks of one entry per thread,
+// entries with the same expert are found within a wave by a ballot match over
+// the key bits; the rank is the popcount of lower lanes; per-wave counts go
+// through LDS to rank across the waves; running[e] (LDS, the rank of the
+// range's first entry of expert e) carries across chunks. have_id0: the
+// caller already holds ids[i0 + tid] in id0.
+template <typename IdT, int NT>
+__device__ void align_scatter_range(const IdT* __restrict__ ids, const float* __restrict__ topk_w, int i0, int i1,
+                                    int K, int E, int block_m, int max_blocks, const int* off_u, const int* off_p,
+                                    int* running, int* wcount, const Dsv4AlignOut& o, bool have_id0,
+                                    long long id0) {
+  constexpr int kWaves = NT / 64;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int nbits = 0;
   while ((1 << nbits) < E + 1) ++nbits;
   const unsigned long long lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  for (int base = 0; base < R; base += kThreads) {
+  for (int base = i0; base < i1; base += NT) {
     const int i = base + tid;
     int e = E;
-    if (i < R) {
-      long long ee = base == 0 ? id0 : (long long)ids[i];
+    if (i < i1) {
+      long long ee = (have_id0 && base == i0) ? id0 : (long long)ids[i];
       if (ee >= 0 && ee < E) e = (int)ee;
     }
     unsigned long long peers = __ballot(1);
@@ -145,7 +143,7 @@ __device__ void align_body(const IdT* __restrict__ ids, const float* __restrict_
     const int rank = __popcll(peers & lt_mask);
     if (rank == 0) wcount[wave * (E + 1) + e] = __popcll(peers);
     __syncthreads();
-    if (i < R && e < E) {
+    if (i < i1 && e < E) {
       int r = running[e] + rank;
       for (int w = 0; w < wave; ++w) r += wcount[w * (E + 1) + e];
       const int u = off_u[e] + r;
@@ -158,13 +156,125 @@ __device__ void align_body(const IdT* __restrict__ ids, const float* __restrict_
       if (o.padded_pos) o.padded_pos[i] = p;
     }
     __syncthreads();
-    for (int ex = tid; ex < E + 1; ex += kThreads) {
+    for (int ex = tid; ex < E + 1; ex += NT) {
       int s = 0;
       for (int w = 0; w < kWaves; ++w) { s += wcount[w * (E + 1) + ex]; wcount[w * (E + 1) + ex] = 0; }
       running[ex] += s;
     }
     __syncthreads();
   }
+}
+
+// One workgroup does it all (decode-sized inputs).
+template <typename IdT, int NT>
+__device__ void align_body(const IdT* __restrict__ ids, const float* __restrict__ topk_w, int R, int K, int E,
+                           int block_m, int max_blocks, const Dsv4AlignOut& o, int n_shared = 0) {
+  constexpr int kWaves = NT / 64;
+  extern __shared__ int lds[];
+  int* cnt = lds;                    // [E + 1] (slot E collects out-of-range ids)
+  int* off_u = cnt + (E + 1);        // [E]
+  int* off_p = off_u + E;            // [E]
+  int* running = off_p + E;          // [E + 1]
+  int* wcount = running + (E + 1);   // [kWaves][E + 1]
+
+  const int tid = threadIdx.x;
+  for (int i = tid; i < E + 1; i += NT) { cnt[i] = 0; running[i] = 0; }
+  for (int i = tid; i < kWaves * (E + 1); i += NT) wcount[i] = 0;
+  __syncthreads();
+
+  // 1. histogram (the first chunk's ids stay in registers for the scatter)
+  const long long id0 = tid < R ? (long long)ids[tid] : 0;
+  for (int i = tid; i < R; i += NT) {
+    long long e = i == tid ? id0 : (long long)ids[i];
+    atomicAdd(&cnt[(e < 0 || e >= E) ? E : (int)e], 1);
+  }
+  __syncthreads();
+
+  // 2. layout (E <= NT)
+  align_layout<NT>(tid < E ? cnt[tid] : 0, cnt[E], R, E, block_m, max_blocks, n_shared, o, off_u, off_p);
+
+  // 3. stable scatter
+  align_scatter_range<IdT, NT>(ids, topk_w, 0, R, K, E, block_m, max_blocks, off_u, off_p, running, wcount, o,
+                               true, id0);
+}
+
+// ---- chunked align for many entries: two launches ------------------------
+// (1) per-chunk counts cc[c][E + 1] (slot E: out-of-range ids), in the same
+//     launch as the quantisation of x; (2) every chunk's workgroup derives the
+//     layout and its own per-expert start from cc and scatters its entries, so
+//     the order is the single-workgroup order (expert ascending, flat index
+//     ascending); workgroup 0 writes the layout outputs.
+constexpr int kAlignChunk = 1024;  // entries per chunk
+
+template <typename IdT, int NT>
+__device__ void align_count_chunk(const IdT* __restrict__ ids, int R, int E, int c, int* cc) {
+  extern __shared__ int lds[];
+  int* cnt = lds;  // [E + 1]
+  for (int i = threadIdx.x; i < E + 1; i += NT) cnt[i] = 0;
+  __syncthreads();
+  const int i1 = min(R, (c + 1) * kAlignChunk);
+  for (int i = c * kAlignChunk + threadIdx.x; i < i1; i += NT) {
+    const long long e = (long long)ids[i];
+    atomicAdd(&cnt[(e < 0 || e >= E) ? E : (int)e], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E + 1; e += NT) cc[(int64_t)c * (E + 1) + e] = cnt[e];
+}
+
+template <typename IdT, int NT, int QF>
+__global__ __launch_bounds__(NT) void align_count_quant_kernel(const IdT* __restrict__ ids, int R, int E, int C,
+                                                               int* __restrict__ cc, const uint4* __restrict__ x,
+                                                               int64_t n_groups, int rule, void* q_codes,
+                                                               void* q_scale) {
+  if ((int)blockIdx.x < C) {
+    align_count_chunk<IdT, NT>(ids, R, E, blockIdx.x, cc);
+    return;
+  }
+  const int64_t g = (int64_t)(blockIdx.x - C) * NT + threadIdx.x;
+  if (QF == 0)
+    dsv4::fp8_quant_group(x, g, g < n_groups, nullptr, (uint2*)q_codes, nullptr, (uint32_t*)q_scale);
+  else if (QF == 1)
+    dsv4::mxfp4_quant_group(x, g, g < n_groups, rule, (uint32_t*)q_codes, (uint8_t*)q_scale, nullptr);
+}
+
+// Every chunk's workgroup sums the chunk counts itself (its exclusive
+// per-expert start and the totals), rebuilds the layout offsets, and scatters
+// its entries; workgroup 0 also writes the layout outputs.
+template <typename IdT, int NT>
+__global__ __launch_bounds__(NT) void align_scatter_kernel(const IdT* __restrict__ ids,
+                                                           const float* __restrict__ topk_w, int R, int K, int E,
+                                                           int C, int block_m, int max_blocks, int n_shared,
+                                                           const int* __restrict__ cc, Dsv4AlignOut o) {
+  constexpr int kWaves = NT / 64;
+  extern __shared__ int lds[];
+  int* off_u = lds;                  // [E]
+  int* off_p = off_u + E;            // [E]
+  int* running = off_p + E;          // [E + 1]
+  int* wcount = running + (E + 1);   // [kWaves][E + 1]
+  __shared__ int bad;
+  const int c = blockIdx.x, tid = threadIdx.x;
+  int tot = 0;  // count of expert tid
+  for (int e = tid; e <= E; e += NT) {
+    int before = 0, all = 0;
+    for (int c0 = 0; c0 < C; c0 += 16) {  // 16 independent loads in flight
+      int v[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = c0 + j < C ? cc[(int64_t)(c0 + j) * (E + 1) + e] : 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        before += c0 + j < c ? v[j] : 0;
+        all += v[j];
+      }
+    }
+    running[e] = before;
+    if (e == tid) tot = all;
+    if (e == E) bad = all;  // slot E: out-of-range ids
+  }
+  for (int i = tid; i < kWaves * (E + 1); i += NT) wcount[i] = 0;
+  __syncthreads();
+  align_layout<NT>(tid < E ? tot : 0, bad, R, E, block_m, max_blocks, n_shared, o, off_u, off_p, c == 0);
+  align_scatter_range<IdT, NT>(ids, topk_w, c * kAlignChunk, min(R, (c + 1) * kAlignChunk), K, E, block_m,
+                               max_blocks, off_u, off_p, running, wcount, o, false, 0);
 }
 
 template <typename IdT, int NT>
@@ -247,5 +357,48 @@ hipError_t launch_moe_align_quant(const void* topk_ids, int ids_int64, const flo
     else { if (qfmt == 0) DSV4_AQ(int32_t, 1024, 0); else DSV4_AQ(int32_t, 1024, 1); }
   }
 #undef DSV4_AQ
+  return hipGetLastError();
+}
+
+int64_t align_chunked_scratch_bytes(int R, int E) {
+  const int64_t C = (R + kAlignChunk - 1) / kAlignChunk;
+  return C * (E + 1) * (int64_t)sizeof(int);
+}
+
+hipError_t launch_moe_align_chunked(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K, int E,
+                                    int block_m, int max_blocks, const Dsv4AlignOut& o, const uint16_t* x,
+                                    int64_t n_elems, int qfmt, int rule, void* q_codes, void* q_scale,
+                                    hipStream_t st, int n_shared, void* scratch) {
+  const int C = (R + kAlignChunk - 1) / kAlignChunk;
+  int* cc = (int*)scratch;
+  const int64_t n_groups = x ? n_elems / 8 : 0;
+  constexpr int NT1 = 256;
+  const int64_t qwg = (n_groups + NT1 - 1) / NT1;
+  if (C + qwg > 0x7fffffffLL) return hipErrorInvalidValue;
+  const dim3 g1((unsigned)(C + qwg));
+  const size_t lds1 = sizeof(int) * (size_t)(E + 1);
+#define DSV4_CQ(IDT, QF)                                                                                    \
+  hipLaunchKernelGGL((align_count_quant_kernel<IDT, NT1, QF>), g1, dim3(NT1), lds1, st, (const IDT*)topk_ids, \
+                     R, E, C, cc, (const uint4*)x, n_groups, rule, q_codes, q_scale)
+  const int qf = x ? qfmt : 2;  // 2: count only
+  if (ids_int64) {
+    if (qf == 0) DSV4_CQ(long long, 0); else if (qf == 1) DSV4_CQ(long long, 1); else DSV4_CQ(long long, 2);
+  } else {
+    if (qf == 0) DSV4_CQ(int32_t, 0); else if (qf == 1) DSV4_CQ(int32_t, 1); else DSV4_CQ(int32_t, 2);
+  }
+#undef DSV4_CQ
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // the layout needs one thread per expert: 256 threads up to 256 experts, 1024 above
+#define DSV4_SC(IDT, NT)                                                                                       \
+  hipLaunchKernelGGL((align_scatter_kernel<IDT, NT>), dim3(C), dim3(NT),                                      \
+                     sizeof(int) * (size_t)(E + E + (E + 1) + (NT / 64) * (E + 1)), st, (const IDT*)topk_ids, \
+                     topk_w, R, K, E, C, block_m, max_blocks, n_shared, cc, o)
+  if (E <= 256) {
+    if (ids_int64) DSV4_SC(long long, 256); else DSV4_SC(int32_t, 256);
+  } else {
+    if (ids_int64) DSV4_SC(long long, 1024); else DSV4_SC(int32_t, 1024);
+  }
+#undef DSV4_SC
   return hipGetLastError();
 }

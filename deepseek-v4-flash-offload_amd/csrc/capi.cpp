@@ -38,6 +38,9 @@ static int hip_status(hipError_t e, const char* where) {
   } while (0)
 
 static inline bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+// Up to this many routed entries one workgroup aligns them (one launch, fused
+// with the quantisation of x in the layer); above it, the chunked two-launch align.
+static constexpr int64_t kAlignSmallRows = 2048;
 static inline int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 extern "C" {
@@ -117,6 +120,39 @@ int dsv4_moe_align(const void* topk_ids, int ids_int64, const float* topk_w, int
                  expert_start, active, num_active, padded_pos, status};
   return hip_status(launch_moe_align(topk_ids, ids_int64, topk_w, (int)R, K, E, block_m, max_blocks, o,
                                      (hipStream_t)stream),
+                    "align launch");
+}
+
+int64_t dsv4_moe_align_workspace_bytes(int T, int K, int E) {
+  if (T <= 0 || K <= 0 || E <= 0) return 0;
+  return align_chunked_scratch_bytes(T * K, E);
+}
+
+int dsv4_moe_align_ws(const void* topk_ids, int ids_int64, const float* topk_w, int T, int K, int E, int block_m,
+                      int max_blocks, int32_t* sorted_ids, int32_t* block_expert, int32_t* num_post_padded,
+                      int32_t* order, int32_t* s_e, float* s_w, int32_t* row, int32_t* counts,
+                      int32_t* expert_start, int32_t* active, int32_t* num_active, int32_t* padded_pos,
+                      int32_t* status, void* workspace, int64_t workspace_bytes, void* stream) {
+  const int64_t R = (int64_t)T * K;
+  if (R <= kAlignSmallRows || workspace == nullptr)
+    return dsv4_moe_align(topk_ids, ids_int64, topk_w, T, K, E, block_m, max_blocks, sorted_ids, block_expert,
+                          num_post_padded, order, s_e, s_w, row, counts, expert_start, active, num_active,
+                          padded_pos, status, stream);
+  REQUIRE(K > 0, DSV4_ERR_SHAPE, "align: bad K=%d", K);
+  REQUIRE(E > 0 && E <= DSV4_MAX_EXPERTS, DSV4_ERR_UNSUPPORTED, "align: E=%d outside 1..%d", E,
+          DSV4_MAX_EXPERTS);
+  REQUIRE(block_m > 0 && block_m <= 1024, DSV4_ERR_SHAPE, "align: block_m=%d", block_m);
+  REQUIRE(R < (1 << 30), DSV4_ERR_SHAPE, "align: too many entries");
+  REQUIRE(max_blocks >= dsv4_moe_align_max_blocks((int)R, E, block_m), DSV4_ERR_SHAPE,
+          "align: max_blocks=%d below the bound %d", max_blocks, dsv4_moe_align_max_blocks((int)R, E, block_m));
+  REQUIRE(sorted_ids && block_expert && num_post_padded && topk_ids, DSV4_ERR_NULL, "align: null pointer");
+  REQUIRE(workspace_bytes >= align_chunked_scratch_bytes((int)R, E) && aligned(workspace, 4), DSV4_ERR_SHAPE,
+          "align: workspace %lld < %lld bytes", (long long)workspace_bytes,
+          (long long)align_chunked_scratch_bytes((int)R, E));
+  Dsv4AlignOut o{sorted_ids, block_expert, num_post_padded, order, s_e, s_w, row, counts,
+                 expert_start, active, num_active, padded_pos, status};
+  return hip_status(launch_moe_align_chunked(topk_ids, ids_int64, topk_w, (int)R, K, E, block_m, max_blocks, o,
+                                             nullptr, 0, 0, 0, nullptr, nullptr, (hipStream_t)stream, 0, workspace),
                     "align launch");
 }
 
@@ -261,7 +297,7 @@ int dsv4_moe_gemm_down(int afmt, const void* a, const void* a_scale, const int32
 // measured to cost far more than the launches they would save. Workspace
 // regions are 256-byte aligned.
 struct LayerWs {
-  int64_t sorted_ids, block_expert, npp, status, xa, xs, h, ha, hs, out, total;
+  int64_t sorted_ids, block_expert, npp, status, xa, xs, h, ha, hs, out, align_scratch, total;
   int max_blocks;
   int bm;
 };
@@ -291,6 +327,7 @@ static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool sha
   w.ha = take(fp8 ? Rt * I : Rt * I / 2);
   w.hs = take(Rt * I / 32);
   w.out = take(2 * Rt * D);
+  w.align_scratch = R > kAlignSmallRows ? take(align_chunked_scratch_bytes((int)R, E)) : 0;
   w.total = o;
   return w;
 }
@@ -332,10 +369,15 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
   // routing layout and the activation quantisation of x share one launch
   Dsv4AlignOut ao{sorted_ids, block_expert, npp, nullptr, nullptr, nullptr, nullptr, nullptr,
                   nullptr,    nullptr,      nullptr, nullptr, status};
-  int rc = hip_status(launch_moe_align_quant(topk_ids, ids_int64, nullptr, R, K, E, bm, w.max_blocks, ao,
-                                             (const uint16_t*)x, (int64_t)T * D, fp8 ? 0 : 1, scale_rule,
-                                             base + w.xa, base + w.xs, (hipStream_t)stream, n_sh),
-                      "align+quant launch");
+  int rc = hip_status(
+      R > kAlignSmallRows
+          ? launch_moe_align_chunked(topk_ids, ids_int64, nullptr, R, K, E, bm, w.max_blocks, ao, (const uint16_t*)x,
+                                     (int64_t)T * D, fp8 ? 0 : 1, scale_rule, base + w.xa, base + w.xs,
+                                     (hipStream_t)stream, n_sh, base + w.align_scratch)
+          : launch_moe_align_quant(topk_ids, ids_int64, nullptr, R, K, E, bm, w.max_blocks, ao, (const uint16_t*)x,
+                                   (int64_t)T * D, fp8 ? 0 : 1, scale_rule, base + w.xa, base + w.xs,
+                                   (hipStream_t)stream, n_sh),
+      "align+quant launch");
   if (rc) return rc;
   const Dsv4ExpertPtrs* table = (const Dsv4ExpertPtrs*)expert_table;
   // gate/up + SwiGLU, quantising h in the epilogue where the kernel holds whole blocks

@@ -47,6 +47,13 @@ hipError_t launch_moe_align_quant(const void* topk_ids, int ids_int64, const flo
                                   int block_m, int max_blocks, const Dsv4AlignOut& o, const uint16_t* x,
                                   int64_t n_elems, int qfmt, int rule, void* q_codes, void* q_scale,
                                   hipStream_t st, int n_shared = 0);
+// The same outputs from two launches for many entries: per-chunk counts (plus
+// the quantisation of x when x is non-null), then per-chunk layout + scatter. scratch: align_chunked_scratch_bytes(R, E) bytes of device memory.
+int64_t align_chunked_scratch_bytes(int R, int E);
+hipError_t launch_moe_align_chunked(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K, int E,
+                                    int block_m, int max_blocks, const Dsv4AlignOut& o, const uint16_t* x,
+                                    int64_t n_elems, int qfmt, int rule, void* q_codes, void* q_scale,
+                                    hipStream_t st, int n_shared, void* scratch);
 hipError_t launch_moe_gather_rows(const uint8_t* src, int64_t n_src, const int32_t* row, int64_t n_rows,
                                   int64_t row_bytes, uint8_t* dst, hipStream_t st);
 // y[t] = bf16( sum over the token's entries, ordered by key, of rows of `src` (bf16) )

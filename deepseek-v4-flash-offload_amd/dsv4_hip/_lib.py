@@ -40,6 +40,9 @@ SIGNATURES = {
                               _i32, _f32, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "dsv4_moe_align_max_blocks": (_i32, [_i32, _i32, _i32]),
     "dsv4_moe_align": (_i32, [_c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32] + [_c_p] * 13 + [_c_p]),
+    "dsv4_moe_align_workspace_bytes": (_i64, [_i32, _i32, _i32]),
+    "dsv4_moe_align_ws": (_i32, [_c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32] + [_c_p] * 13
+                          + [_c_p, _i64, _c_p]),
     "dsv4_moe_permute": (_i32, [_c_p, _i64, _c_p, _i64, _i64, _c_p, _c_p]),
     "dsv4_moe_unpermute_workspace_bytes": (_i64, [_i32, _i32]),
     "dsv4_moe_unpermute": (_i32, [_c_p, _c_p, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p]),

@@ -221,10 +221,12 @@ def moe_align(topk_ids: torch.Tensor, topk_w: Optional[torch.Tensor], n_experts:
         counts=torch.empty(n_experts, **i32), expert_start=torch.empty(n_experts, **i32),
         active=torch.empty(n_experts, **i32), num_active=torch.empty(1, **i32),
         padded_pos=torch.empty(R, **i32), status=torch.empty(1, **i32))
-    call("dsv4_moe_align", _p(ids), 1 if ids.dtype == torch.int64 else 0, _p(w), T, K, n_experts, block_m, mb,
+    nws = int(_lib.lib().dsv4_moe_align_workspace_bytes(T, K, n_experts))
+    ws = torch.empty(max(nws, 4), dtype=torch.uint8, device=dev)
+    call("dsv4_moe_align_ws", _p(ids), 1 if ids.dtype == torch.int64 else 0, _p(w), T, K, n_experts, block_m, mb,
          _p(res.sorted_ids), _p(res.block_expert), _p(res.num_post_padded), _p(res.order), _p(res.s_e),
          _p(res.s_w if w is not None else None), _p(res.row), _p(res.counts), _p(res.expert_start),
-         _p(res.active), _p(res.num_active), _p(res.padded_pos), _p(res.status), _stream(ids))
+         _p(res.active), _p(res.num_active), _p(res.padded_pos), _p(res.status), _p(ws), ws.numel(), _stream(ids))
     if w is None:
         res.s_w.zero_()
     return res

@@ -121,6 +121,18 @@ int dsv4_moe_align(const void* topk_ids, int ids_int64, const float* topk_w, int
                    int32_t* order, int32_t* s_e, float* s_w, int32_t* row, int32_t* counts, int32_t* expert_start,
                    int32_t* active, int32_t* num_active, int32_t* padded_pos, int32_t* status, void* stream);
 
+/* dsv4_moe_align with a workspace (dsv4_moe_align_workspace_bytes(T, K, E) bytes):
+ * above 2048 entries the work is split over chunks of 1024 entries in two
+ * launches (per-chunk counts; per-chunk layout and stable scatter) instead of
+ * one workgroup; same outputs, bit for bit. A NULL workspace or at
+ * most 2048 entries: the single-workgroup dsv4_moe_align. */
+int64_t dsv4_moe_align_workspace_bytes(int T, int K, int E);
+int dsv4_moe_align_ws(const void* topk_ids, int ids_int64, const float* topk_w, int T, int K, int E, int block_m,
+                      int max_blocks, int32_t* sorted_ids, int32_t* block_expert, int32_t* num_post_padded,
+                      int32_t* order, int32_t* s_e, float* s_w, int32_t* row, int32_t* counts,
+                      int32_t* expert_start, int32_t* active, int32_t* num_active, int32_t* padded_pos,
+                      int32_t* status, void* workspace, int64_t workspace_bytes, void* stream);
+
 /* dst[i] = src[row[i]] for rows of row_bytes bytes (multiple of 16); src has
  * n_src rows and a row index outside [0, n_src) yields a zero row.
  * Replaces the gathers x_sorted = xq[row] (deepseek_v4.py:171, 213-214). */

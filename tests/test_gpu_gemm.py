@@ -132,11 +132,12 @@ def test_grouped_gemm_empty_group_pattern(gpu):
 
 @pytest.mark.parametrize("profile", ["bf16", "a4w4"])
 @pytest.mark.parametrize("T,K,E,D,I", [(8, 8, 256, 4096, 2048), (64, 6, 32, 1024, 512), (100, 6, 32, 1024, 512),
-                                       (256, 8, 32, 2048, 1024)])
+                                       (256, 8, 32, 2048, 1024), (400, 8, 256, 1024, 512)])
 def test_layer_forward_vs_oracle(gpu, profile, T, K, E, D, I):
     # 16-row blocks up to 2047 routed rows (h quantised in the gate/up epilogue for a4w4,
     # by a separate launch for FP8); 256 tokens x top-8 = 2048 routed rows: 64-row M blocks
-    # (tiled kernel, h quantised in the epilogue in both profiles)
+    # (tiled kernel, h quantised in the epilogue in both profiles); 3200 routed rows: the
+    # chunked two-launch align
     ids, w, xb, host, devw, table = _case(T, K, E, D, I, 77 + T, gpu)
     runner = ops.LayerRunner(gpu, E, D, I)
     x = _dev_bf16(xb, gpu)

@@ -49,9 +49,10 @@ def test_expand_block_scales_bit_exact(gpu, n, k):
 
 
 # (T, K, E, D, I): decode at full size, small shapes, 2048 routed rows (64-row
-# blocks, tiled kernel, h quantised in its epilogue), one token
+# blocks, tiled kernel, h quantised in its epilogue), one token, 2400 routed
+# rows (chunked align with the shared group)
 CASES = [(8, 8, 256, 4096, 2048), (24, 4, 16, 1024, 512), (256, 8, 16, 1024, 512),
-         (300, 6, 24, 2048, 1024), (1, 8, 64, 1024, 512)]
+         (300, 6, 24, 2048, 1024), (1, 8, 64, 1024, 512), (300, 8, 64, 1024, 512)]
 
 
 @pytest.mark.parametrize("T,K,E,D,I", CASES)
