@@ -442,11 +442,11 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
   }
   rc = hip_status(launch_moe_gemm_down(dn, (hipStream_t)stream), "gemm down launch");
   if (rc) return rc;
-  if (!shared) return dsv4_moe_combine(base + w.out, topk_ids, ids_int64, T, K, D, y, stream);
+  // ids outside [0, E) were skipped by the align (never computed) and add nothing here
   REQUIRE(aligned(y, 16), DSV4_ERR_SHAPE, "layer: y not 16-byte aligned");
   const uint16_t* outp = (const uint16_t*)(base + w.out);
   return hip_status(launch_moe_combine_flat(outp, topk_ids, ids_int64, T, K, D, (uint16_t*)y, (hipStream_t)stream,
-                                            outp + (int64_t)R * D),
+                                            shared ? outp + (int64_t)R * D : nullptr, E),
                     "combine launch");
 }
 

@@ -68,17 +68,20 @@ DSV4_DEV int wave_select_rank(int rank, int n, int r) {
 // shared rows (the shared expert's output, bf16 [T, D]) the routed sum is
 // rounded to bf16 first and the shared row added to it, as the reference's
 // `out + self.shared_experts(hs)` adds two bf16 tensors (deepseek_v4.py:262-264).
+// Entries whose id is outside [0, E) were never aligned (moe_align counts them
+// in its status) and contribute nothing.
 template <typename IdT>
 __global__ __launch_bounds__(64) void combine_flat_kernel(const u32x4* __restrict__ src,
                                                           const IdT* __restrict__ ids, int K, int D,
                                                           u32x4* __restrict__ y,
-                                                          const u32x4* __restrict__ shared_rows) {
+                                                          const u32x4* __restrict__ shared_rows, int E) {
   const int t = blockIdx.y;
   const int lane = threadIdx.x;
   const long long key = lane < K ? (long long)ids[(int64_t)t * K + lane] : 0;
   const int rank = wave_rank(key, K);
   // lane r receives the k of rank r (the inverse permutation, pushed by ds_permute)
   const int k_of_rank = __builtin_amdgcn_ds_permute((lane < K ? rank : lane) * 4, lane);
+  const int valid = (key >= 0 && key < E) ? 1 : 0;
   const int vecs = D / 8;
   const int c = blockIdx.x * 64 + lane;
   const bool live = c < vecs;
@@ -90,7 +93,8 @@ __global__ __launch_bounds__(64) void combine_flat_kernel(const u32x4* __restric
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int k = __shfl(k_of_rank, min(r0 + i, K - 1), 64);
-      v[i] = (r0 + i < K) ? srow[(int64_t)k * vecs] : u32x4{0u, 0u, 0u, 0u};
+      const bool use = r0 + i < K && __shfl(valid, k, 64) != 0;
+      v[i] = use ? srow[(int64_t)k * vecs] : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i)
@@ -166,15 +170,15 @@ hipError_t launch_moe_gather_rows(const uint8_t* src, int64_t n_src, const int32
 }
 
 hipError_t launch_moe_combine_flat(const uint16_t* src, const void* topk_ids, int ids_int64, int T, int K,
-                                   int D, uint16_t* y, hipStream_t st, const uint16_t* shared_rows) {
+                                   int D, uint16_t* y, hipStream_t st, const uint16_t* shared_rows, int E) {
   if (T == 0 || D == 0) return hipSuccess;
   const dim3 grid((D / 8 + 63) / 64, T);
   if (ids_int64)
     hipLaunchKernelGGL(combine_flat_kernel<long long>, grid, dim3(64), 0, st, (const u32x4*)src,
-                       (const long long*)topk_ids, K, D, (u32x4*)y, (const u32x4*)shared_rows);
+                       (const long long*)topk_ids, K, D, (u32x4*)y, (const u32x4*)shared_rows, E);
   else
     hipLaunchKernelGGL(combine_flat_kernel<int32_t>, grid, dim3(64), 0, st, (const u32x4*)src,
-                       (const int32_t*)topk_ids, K, D, (u32x4*)y, (const u32x4*)shared_rows);
+                       (const int32_t*)topk_ids, K, D, (u32x4*)y, (const u32x4*)shared_rows, E);
   return hipGetLastError();
 }
 

@@ -59,8 +59,10 @@ hipError_t launch_moe_gather_rows(const uint8_t* src, int64_t n_src, const int32
 // y[t] = bf16( sum over the token's entries, ordered by key, of rows of `src` (bf16) )
 // mode 0: entry (t,k) -> src row t*K+k, key = topk_ids[t,k]   (flat-order combine)
 // mode 1: entries from a per-token position list built from `row`, key = position
+// Entries with ids outside [0, E) contribute nothing (E = INT_MAX: every id counts).
 hipError_t launch_moe_combine_flat(const uint16_t* src, const void* topk_ids, int ids_int64, int T, int K,
-                                   int D, uint16_t* y, hipStream_t st, const uint16_t* shared_rows = nullptr);
+                                   int D, uint16_t* y, hipStream_t st, const uint16_t* shared_rows = nullptr,
+                                   int E = 0x7fffffff);
 // out[n][k/32] = block[n/128][k/128]: 128x128 E8M0 block scales repeated per 32 along K
 hipError_t launch_expand_block_scales(const uint8_t* block, int64_t N, int64_t K, uint8_t* out, hipStream_t st);
 hipError_t launch_moe_unpermute_rows(const uint16_t* src, const int32_t* row, int R, int T, int Kmax, int D,

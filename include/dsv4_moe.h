@@ -184,7 +184,11 @@ int dsv4_moe_gemm_down(int afmt, const void* a, const void* a_scale, const int32
  * profile below 2048 routed rows). M blocks of 16 rows below 2048 routed rows,
  * 64 from there on. x [T, D] bf16, topk_ids/topk_w [T, K], y [T, D] bf16.
  * scale_rule applies to the A4W4 profile only. The workspace (size from
- * dsv4_moe_layer_workspace_bytes, 256-byte aligned) needs no initialisation. */
+ * dsv4_moe_layer_workspace_bytes, 256-byte aligned) needs no initialisation.
+ * A routed entry whose id is outside [0, E) contributes nothing (the
+ * reference's engine lookup raises for it; check ids with dsv4_moe_align's
+ * status where that matters), and an expert whose table entry holds null
+ * weight pointers contributes zeros. */
 int dsv4_moe_layer_workspace_bytes(int T, int K, int E, int D, int I, int profile, int64_t* bytes);
 int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
                            const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
