@@ -5,8 +5,10 @@
 //   w      = scores[ids], / sum(w) when renormalising, * routed_scaling_factor
 //
 // Two launches:
-//   route_logits_kernel - fp32 MFMA (v_mfma_f32_16x16x4_f32), one wave per
-//     16x16 (small T) or 32x32 (T >= 256) tokens x experts x one K chunk. K is
+//   route_logits_kernel - fp32 MFMA (v_mfma_f32_16x16x4_f32), or for bf16 x
+//     from 256 tokens on bf16 MFMA on an exact three-way bf16 split of the
+//     weight, one wave per
+//     16x16 (small T) or 64x32 (T >= 256) tokens x experts x one K chunk. K is
 //     split into S chunks so that enough waves run (decode-sized T has few
 //     tiles to stream the 4 MiB gate matrix with); each chunk's partial logits
 //     go to the workspace [S, T, E].
@@ -20,6 +22,7 @@ namespace dsv4 {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kRouteWaves = 4;  // waves per workgroup in both kernels
 
@@ -31,7 +34,15 @@ constexpr int kRouteWaves = 4;  // waves per workgroup in both kernels
 // {kb + 8g + i : g = 0..3}; the 8 MFMAs of a step cover [kb, kb+32).
 // XF32: x is fp32 (the reference takes hs.float(), so fp32 hidden states are
 // used as they are); otherwise bf16.
-template <bool XF32, int MT, int NT>
+//
+// BF3 (bf16 x only): each fp32 weight w is split exactly into three bf16
+// planes, hi = w with its low 16 bits cleared, mid = the same of w - hi, lo =
+// w - hi - mid (at most 8 significant bits left, so exact in bf16), and the
+// step's 32 k run as three v_mfma_f32_16x16x32_bf16 (A = the bf16 x values, B
+// = hi, mid, lo): every product is exact in fp32 and the accumulation is fp32,
+// at about five times the fp32 MFMA's rate. Lane (r, g) feeds the same 8 k's
+// to A and B, so the hardware's pairing of A and B elements is all that matters.
+template <bool XF32, int MT, int NT, bool BF3 = false>
 __global__ __launch_bounds__(64 * kRouteWaves) void route_logits_kernel(const void* __restrict__ xp,
                                                                          const float* __restrict__ w, int T,
                                                                          int D, int E, int kchunk,
@@ -79,9 +90,11 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_logits_kernel(const vo
   for (int n = 0; n < NT; ++n) wa[n] = *(const float4*)wr[n], wb[n] = *(const float4*)(wr[n] + 4);
   for (int kb = 0; kb < kchunk; kb += 32) {
     float xf[MT][8], wf[NT][8];
+    uint4 xa_cur[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       const uint4 u = xa[m], v = xb[m];
+      xa_cur[m] = u;
       if (XF32) {
         xf[m][0] = __uint_as_float(u.x), xf[m][1] = __uint_as_float(u.y);
         xf[m][2] = __uint_as_float(u.z), xf[m][3] = __uint_as_float(u.w);
@@ -106,13 +119,48 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_logits_kernel(const vo
       for (int n = 0; n < NT; ++n)
         wa[n] = *(const float4*)(wr[n] + kb + 32), wb[n] = *(const float4*)(wr[n] + kb + 36);
     }
+    if constexpr (BF3) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+      for (int n = 0; n < NT; ++n) {
+        uint32_t hi[4], mid[4], lo[4];
 #pragma unroll
-      for (int m = 0; m < MT; ++m)
+        for (int i = 0; i < 4; ++i) {
+          uint32_t h2[2], m2[2], l2[2];
 #pragma unroll
-        for (int n = 0; n < NT; ++n)
-          acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[m][i], wf[n][i], acc[m][n], 0, 0, 0);
+          for (int h = 0; h < 2; ++h) {
+            const float w = wf[n][2 * i + h];
+            const uint32_t wh = __float_as_uint(w) & 0xffff0000u;
+            const float r1 = w - __uint_as_float(wh);
+            const uint32_t wm = __float_as_uint(r1) & 0xffff0000u;
+            const float r2 = r1 - __uint_as_float(wm);
+            h2[h] = wh >> 16;
+            m2[h] = wm >> 16;
+            l2[h] = __float_as_uint(r2) >> 16;
+          }
+          hi[i] = h2[0] | (h2[1] << 16);
+          mid[i] = m2[0] | (m2[1] << 16);
+          lo[i] = l2[0] | (l2[1] << 16);
+        }
+        const bf16x8 bh = __builtin_bit_cast(bf16x8, make_uint4(hi[0], hi[1], hi[2], hi[3]));
+        const bf16x8 bm = __builtin_bit_cast(bf16x8, make_uint4(mid[0], mid[1], mid[2], mid[3]));
+        const bf16x8 bl = __builtin_bit_cast(bf16x8, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const bf16x8 a = __builtin_bit_cast(bf16x8, xa_cur[m]);
+          acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl, acc[m][n], 0, 0, 0);
+          acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bm, acc[m][n], 0, 0, 0);
+          acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh, acc[m][n], 0, 0, 0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+          for (int n = 0; n < NT; ++n)
+            acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[m][i], wf[n][i], acc[m][n], 0, 0, 0);
+    }
   }
   // C lane l holds C[4(l/16) + i][l%16]: token t0 + 16m + 4g + i, expert e0 + 16n + r.
   float* out = part + (int64_t)z * T * E;
@@ -167,13 +215,23 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(const floa
   if (t >= T) return;
   const float ninf = -__builtin_inff();
   float sc[EPL];
+  // the S partials of each expert, summed in chunk order; up to 16 chunks' loads in flight
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const int e = lane + 64 * j;
-    float l = 0.f;
-    if (e < E)
-      for (int z = 0; z < S; ++z) l += part[((int64_t)z * T + t) * E + e];
-    sc[j] = l;
+  for (int j = 0; j < EPL; ++j) sc[j] = 0.f;
+  for (int z0 = 0; z0 < S; z0 += 16) {
+    float v[16][EPL];
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) {
+        const int e = lane + 64 * j;
+        v[i][j] = (z0 + i < S && e < E) ? part[((int64_t)(z0 + i) * T + t) * E + e] : 0.f;
+      }
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int j = 0; j < EPL; ++j)
+        if (z0 + i < S) sc[j] += v[i][j];
   }
   if (scoring == 0) {  // softmax over the E experts
     float m = ninf;
@@ -265,15 +323,20 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(const floa
 
 using namespace dsv4;
 
-// Per-wave tile: 16 x 16 for decode-sized T (more waves, shorter K loops),
-// 32 x 32 from 256 tokens on (half the L2 bytes per MFMA).
-static int route_tile(int T) { return T >= 256 ? 2 : 1; }
+// Per-wave tile: 16 tokens x 16 experts for decode-sized T (more waves,
+// shorter K loops); from 256 tokens on 64 x 32 (each weight fragment serves
+// four token tiles, which halves the L2 bytes the gate weight costs).
+struct RouteTile {
+  int mt, nt;
+};
+static RouteTile route_tile(int T) { return T >= 256 ? RouteTile{4, 2} : RouteTile{1, 1}; }
 
 // K split so that about 2048 waves (two per SIMD) run, with chunks of at least
 // 256 k that stay multiples of 32.
 int route_split_k(int T, int D, int E) {
-  const int tt = 16 * route_tile(T);
-  const int tiles = ((E + tt - 1) / tt) * ((T + tt - 1) / tt);
+  const RouteTile rt = route_tile(T);
+  const int tt = 16 * rt.mt, te = 16 * rt.nt;
+  const int tiles = ((E + te - 1) / te) * ((T + tt - 1) / tt);
   int S = 1;
   while (S < 16 && tiles * S < 2048 && D % (64 * S) == 0 && D / (2 * S) >= 256) S *= 2;
   return S;
@@ -284,14 +347,16 @@ hipError_t launch_moe_route(const void* x, int x_f32, const float* gate_w, int T
                             int ids_is64, int64_t vocab, int renorm, float scale, float* out_w,
                             int32_t* out_ids, int32_t* status, float* part, hipStream_t st) {
   const int S = route_split_k(T, D, E);
-  const int mt = route_tile(T), tt = 16 * mt;
-  dim3 g1((E + tt * kRouteWaves - 1) / (tt * kRouteWaves), (T + tt - 1) / tt, S);
+  const RouteTile rt = route_tile(T);
+  const int tt = 16 * rt.mt, te = 16 * rt.nt;
+  dim3 g1((E + te * kRouteWaves - 1) / (te * kRouteWaves), (T + tt - 1) / tt, S);
   dim3 b1(64 * kRouteWaves);
-  if (mt == 2) {
+  if (rt.mt == 4) {
     if (x_f32)
-      hipLaunchKernelGGL((route_logits_kernel<true, 2, 2>), g1, b1, 0, st, x, gate_w, T, D, E, D / S, part);
+      hipLaunchKernelGGL((route_logits_kernel<true, 4, 2>), g1, b1, 0, st, x, gate_w, T, D, E, D / S, part);
     else
-      hipLaunchKernelGGL((route_logits_kernel<false, 2, 2>), g1, b1, 0, st, x, gate_w, T, D, E, D / S, part);
+      hipLaunchKernelGGL((route_logits_kernel<false, 4, 2, true>), g1, b1, 0, st, x, gate_w, T, D, E, D / S,
+                         part);
   } else {
     if (x_f32)
       hipLaunchKernelGGL((route_logits_kernel<true, 1, 1>), g1, b1, 0, st, x, gate_w, T, D, E, D / S, part);

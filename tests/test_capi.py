@@ -123,7 +123,7 @@ def test_route_validation():
     rc, msg = route()
     assert rc == -1 and "null" in msg
     assert route(T=0)[0] == 0  # no tokens is a no-op
-    # the partial-logit workspace [S, T, E]: K split 16 ways at decode sizes, 4 ways at 2048 tokens
+    # the partial-logit workspace [S, T, E]: K split 16 ways at decode sizes, 8 ways at 2048 tokens
     assert lib.dsv4_moe_route_workspace_bytes(8, 4096, 256) == 16 * 8 * 256 * 4
-    assert lib.dsv4_moe_route_workspace_bytes(2048, 4096, 256) == 4 * 2048 * 256 * 4
+    assert lib.dsv4_moe_route_workspace_bytes(2048, 4096, 256) == 8 * 2048 * 256 * 4
     assert lib.dsv4_moe_route_workspace_bytes(0, 4096, 256) == 0
