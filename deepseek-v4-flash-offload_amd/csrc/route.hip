@@ -183,16 +183,41 @@ DSV4_DEV float wave_sum(float v) {
   return v;
 }
 
-// (value, id) maximum over the wave; equal values go to the lower id.
+DSV4_DEV bool better(float ov, int oid, float v, int id) { return ov > v || (ov == v && oid < id); }
+
+// One DPP step of the (value, id) reduction: the partner lane given by CTRL.
+template <int CTRL>
+DSV4_DEV void argmax_dpp(float& v, int& id) {
+  const float ov = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+  const int oid = __builtin_amdgcn_update_dpp(0, id, CTRL, 0xf, 0xf, false);
+  if (better(ov, oid, v, id)) {
+    v = ov;
+    id = oid;
+  }
+}
+
+// (value, id) maximum over the wave, uniform result; equal values go to the
+// lower id. Within each 16-lane row: quad swaps (xor 1, xor 2), then the half-row
+// and row mirrors (each lane meets the other quad, then the other half); the
+// four rows' results are then read as scalars.
 DSV4_DEV void wave_argmax(float& v, int& id) {
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(v, o, 64);
-    const int oid = __shfl_xor(id, o, 64);
-    if (ov > v || (ov == v && oid < id)) {
-      v = ov;
-      id = oid;
+  argmax_dpp<0xb1>(v, id);   // quad_perm [1, 0, 3, 2]
+  argmax_dpp<0x4e>(v, id);   // quad_perm [2, 3, 0, 1]
+  argmax_dpp<0x141>(v, id);  // row_half_mirror
+  argmax_dpp<0x140>(v, id);  // row_mirror
+  float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  int bid = __builtin_amdgcn_readlane(id, 0);
+#pragma unroll
+  for (int r = 1; r < 4; ++r) {
+    const float rv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16 * r));
+    const int rid = __builtin_amdgcn_readlane(id, 16 * r);
+    if (better(rv, rid, bv, bid)) {
+      bv = rv;
+      bid = rid;
     }
   }
+  v = bv;
+  id = bid;
 }
 
 DSV4_DEV int64_t load_index(const void* p, int is64, int64_t i) {
@@ -301,7 +326,7 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_topk_kernel(const floa
 #pragma unroll
       for (int j = 1; j < EPL; ++j)
         if ((id >> 6) == j) mine = sc[j];
-      wk = __shfl(mine, id & 63, 64);
+      wk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), id & 63));  // id is wave-uniform
     }
     sum += wk;
     if (lane == k) {
