@@ -190,9 +190,22 @@ def measure_dequant(dev, gen, n_mats=64, reps=5):
     e1.synchronize()
     tb = e0.elapsed_time(e1) * 1e-3 / reps
     gbs_b = per * n_mats / tb / 1e9
+    # config-0 GEMV (bf16 x [1, 4096] @ dequant(W)^T) over the same 64 matrices as one
+    # [1, 64*2048] launch: weight bytes (packed + scales) + x + y per launch
+    x = torch.randn(1, K, device=dev, generator=gen).to(torch.bfloat16)
+    ops.mxfp4_gemv(x, big_p, big_s)
+    e0.record()
+    for _ in range(reps):
+        ops.mxfp4_gemv(x, big_p, big_s)
+    e1.record()
+    e1.synchronize()
+    tg = e0.elapsed_time(e1) * 1e-3 / reps
+    gemv_bytes = n_mats * N * (K // 2 + K // 32) + 2 * K + 2 * n_mats * N
     return {"gbs": gbs_b, "frac_hbm": gbs_b / HBM_PEAK_GBS, "batched_us": tb * 1e6,
             "per_matrix_call_gbs": per / t / 1e9, "us_per_matrix_call": t * 1e6,
-            "bytes_per_matrix": per, "matrices": n_mats}
+            "bytes_per_matrix": per, "matrices": n_mats,
+            "gemv_batched_us": tg * 1e6, "gemv_gbs": gemv_bytes / tg / 1e9,
+            "gemv_frac_hbm": gemv_bytes / tg / 1e9 / HBM_PEAK_GBS}
 
 
 def measure_pcie(dev, record_bytes):

@@ -62,6 +62,19 @@ int dsv4_mxfp4_dequant_bf16(const void* packed, const void* scales, void* out, i
                     "dequant launch");
 }
 
+int dsv4_mxfp4_gemv_bf16(const void* x, int m, const void* packed, const void* scales, int n, int k, void* y,
+                         void* stream) {
+  REQUIRE(m >= 0 && n >= 0 && k >= 0, DSV4_ERR_SHAPE, "gemv: negative size");
+  REQUIRE(m <= 16, DSV4_ERR_UNSUPPORTED, "gemv: %d activation rows (at most 16)", m);
+  REQUIRE(k > 0 && k % 32 == 0, DSV4_ERR_SHAPE, "gemv: K=%d must be a positive multiple of 32", k);
+  if (m == 0 || n == 0) return DSV4_OK;
+  REQUIRE(x && packed && scales && y, DSV4_ERR_NULL, "gemv: null pointer");
+  REQUIRE(aligned(x, 16) && aligned(packed, 16), DSV4_ERR_SHAPE, "gemv: x and packed need 16-byte alignment");
+  return hip_status(launch_mxfp4_gemv((const uint16_t*)x, m, (const uint8_t*)packed, (const uint8_t*)scales, n, k,
+                                      (uint16_t*)y, (hipStream_t)stream),
+                    "gemv launch");
+}
+
 int dsv4_fp8_act_quant(const void* x, int64_t rows, int64_t cols, int block_size, void* rt, void* codes,
                        void* scale_f32, void* scale_e8m0x4, void* stream) {
   REQUIRE(rows >= 0 && cols >= 0, DSV4_ERR_SHAPE, "act_quant: negative size");

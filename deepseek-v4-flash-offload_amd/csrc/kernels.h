@@ -16,6 +16,9 @@ struct Dsv4ExpertPtrs {
 
 hipError_t launch_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, uint16_t* out,
                                 int64_t n_elems, hipStream_t st);
+// y[M, N] = bf16(x[M, K] @ dequant(packed, scales)^T), fp32 accumulation, M <= 16
+hipError_t launch_mxfp4_gemv(const uint16_t* x, int M, const uint8_t* packed, const uint8_t* scales, int N, int K,
+                             uint16_t* y, hipStream_t st);
 hipError_t launch_fp8_act_quant(const uint16_t* x, int64_t n_elems, uint16_t* rt, uint8_t* codes,
                                 float* scale_f32, uint8_t* scale_e8m0x4, hipStream_t st);
 hipError_t launch_mxfp4_act_quant(const uint16_t* x, int64_t n_elems, int rule, uint8_t* packed,

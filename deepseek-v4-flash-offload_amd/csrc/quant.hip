@@ -103,6 +103,119 @@ __global__ __launch_bounds__(256) void mxfp4_act_quant_kernel(const uint4* __res
 // ---------------------------------------------------------------------------
 // launchers
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// y[m] = bf16(x[m] @ dequant(W)^T) for a few activation rows (the config-0
+// "dequant + bf16 GEMV" of the reference's CPU path: npu_ops.py:142-158 then
+// F.linear). One wave per kGemvRows weight rows: per pass lane L takes 32-element
+// block L (+64 per pass) of every one of its rows - the rows' 16 packed bytes
+// and E8M0 byte are all loaded before any is used, so kGemvRows loads per lane
+// are in flight - decodes them with the hardware scaled fp4 -> fp32 convert
+// (exact) and accumulates x * w in fp32; wave sums give the dot products. x stays bf16 (no activation
+// quantisation). HBM-bound on the weight bytes.
+// ---------------------------------------------------------------------------
+constexpr int kGemvRows = 8;
+
+template <int MB>
+__global__ __launch_bounds__(256) void mxfp4_gemv_kernel(const uint16_t* __restrict__ x, int M,
+                                                         const uint8_t* __restrict__ packed,
+                                                         const uint8_t* __restrict__ scales, int N, int K,
+                                                         uint16_t* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * kGemvRows;
+  if (n0 >= N) return;
+  const int nblk = K / 32;
+  float acc[kGemvRows][MB];
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r)
+#pragma unroll
+    for (int m = 0; m < MB; ++m) acc[r][m] = 0.f;
+  for (int b = lane; b < nblk; b += 64) {
+    u32x4 p[kGemvRows];
+    uint32_t sb[kGemvRows];
+#pragma unroll
+    for (int r = 0; r < kGemvRows; ++r) {
+      const int n = min(n0 + r, N - 1);  // rows past N repeat the last row; never stored
+      p[r] = *(const u32x4*)(packed + (int64_t)n * (K / 2) + 16 * b);
+      sb[r] = scales[(int64_t)n * nblk + b];
+    }
+    uint32_t xw[MB][16];  // the x rows' 32 bf16 values of this block, packed
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      const u32x4* xr = (const u32x4*)(x + (int64_t)min(m, M - 1) * K + 32 * b);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x4 v = xr[c];
+        xw[m][4 * c] = v.x, xw[m][4 * c + 1] = v.y, xw[m][4 * c + 2] = v.z, xw[m][4 * c + 3] = v.w;
+      }
+    }
+    // one x row: its 32 floats once per block; more rows: converted where used
+    float xf1[32];
+    if constexpr (MB == 1) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        xf1[2 * j] = bf16_to_f32(xw[0][j] & 0xffffu);
+        xf1[2 * j + 1] = bf16_to_f32(xw[0][j] >> 16);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kGemvRows; ++r) {
+      // hardware scaled convert: 2 nibbles (low first) -> LUT * 2^(s-127) in fp32, exact
+      // (nibble 8 gives -0.0 where the table holds +0.0: the same contribution to a sum)
+      const float sc = e8m0_to_f32(sb[r]);
+      const uint32_t pw[4] = {p[r].x, p[r].y, p[r].z, p[r].w};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        const f32x2 w0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(pw[q], sc, 0);
+        const f32x2 w1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(pw[q], sc, 1);
+        const f32x2 w2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(pw[q], sc, 2);
+        const f32x2 w3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(pw[q], sc, 3);
+        const float wv[8] = {w0.x, w0.y, w1.x, w1.y, w2.x, w2.y, w3.x, w3.y};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+#pragma unroll
+          for (int m = 0; m < MB; ++m) {
+            float xv;
+            if constexpr (MB == 1) {
+              xv = xf1[8 * q + i];
+            } else {
+              const uint32_t d = xw[m][4 * q + i / 2];
+              xv = bf16_to_f32((i & 1) ? (d >> 16) : (d & 0xffffu));
+            }
+            acc[r][m] = fmaf(xv, wv[i], acc[r][m]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < kGemvRows; ++r)
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      float v = acc[r][m];
+      for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+      if (lane == 0 && m < M && n0 + r < N) y[(int64_t)m * N + n0 + r] = (uint16_t)f32_to_bf16(v);
+    }
+}
+
+// M = 1 or up to 4 rows per launch; more rows run as several launches
+hipError_t launch_mxfp4_gemv(const uint16_t* x, int M, const uint8_t* packed, const uint8_t* scales, int N, int K,
+                             uint16_t* y, hipStream_t st) {
+  const dim3 grid((N + 4 * kGemvRows - 1) / (4 * kGemvRows));
+  for (int m0 = 0; m0 < M; m0 += 4) {
+    const int mc = min(4, M - m0);
+    const uint16_t* xm = x + (int64_t)m0 * K;
+    uint16_t* ym = y + (int64_t)m0 * N;
+    if (mc == 1)
+      hipLaunchKernelGGL((mxfp4_gemv_kernel<1>), grid, dim3(256), 0, st, xm, mc, packed, scales, N, K, ym);
+    else
+      hipLaunchKernelGGL((mxfp4_gemv_kernel<4>), grid, dim3(256), 0, st, xm, mc, packed, scales, N, K, ym);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
 hipError_t launch_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, uint16_t* out,
                                 int64_t n_elems, hipStream_t st) {
   const int64_t n_groups = n_elems / 8;

@@ -33,6 +33,7 @@ SIGNATURES = {
     "dsv4_last_error": (ctypes.c_char_p, []),
     "dsv4_abi_version": (_i32, []),
     "dsv4_mxfp4_dequant_bf16": (_i32, [_c_p, _c_p, _c_p, _i64, _i64, _c_p]),
+    "dsv4_mxfp4_gemv_bf16": (_i32, [_c_p, _i32, _c_p, _c_p, _i32, _i32, _c_p, _c_p]),
     "dsv4_fp8_act_quant": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "dsv4_mxfp4_act_quant": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p]),
     "dsv4_moe_route_workspace_bytes": (_i64, [_i32, _i32, _i32]),

@@ -59,6 +59,20 @@ def dequant_mxfp4(w_packed: torch.Tensor, scale: torch.Tensor, out: Optional[tor
     return out
 
 
+def mxfp4_gemv(x: torch.Tensor, w_packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """``bf16(x @ dequant(W)^T)`` for up to 16 bf16 rows of x, fp32 accumulation."""
+    _dev(x, "mxfp4_gemv")
+    x = x.to(torch.bfloat16).contiguous()
+    wp, sc = _u8(w_packed), _u8(scale)
+    M, K = x.shape
+    N = wp.shape[0]
+    if wp.shape[1] * 2 != K or sc.shape != (N, K // 32):
+        raise ValueError(f"mxfp4_gemv: weight {tuple(wp.shape)} / scales {tuple(sc.shape)} do not match K={K}")
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+    call("dsv4_mxfp4_gemv_bf16", _p(x), M, _p(wp), _p(sc), N, K, _p(y), _stream(x))
+    return y
+
+
 def fp8_act_quant(x: torch.Tensor, block_size: int = 128, rt: Optional[torch.Tensor] = None,
                   want_codes: bool = False, want_scale: bool = False, want_e8m0x4: bool = False):
     """Per-128 FP8 E4M3 quantisation of a bf16 tensor (last dim blocked).

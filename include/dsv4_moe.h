@@ -65,6 +65,14 @@ int dsv4_abi_version(void);
 int dsv4_mxfp4_dequant_bf16(const void* packed, const void* scales, void* out, int64_t n_rows, int64_t k,
                             void* stream);
 
+/* y[m, n] = bf16(sum_k x[m, k] * dequant(packed, scales)[n, k]) with fp32
+ * accumulation: the reference's CPU "dequant_fp4_weight + F.linear" check of a
+ * single MXFP4 matrix (npu_ops.py:142-158), x kept in bf16 (no activation
+ * quantisation). x bf16 [m, k] (m <= 16), packed [n, k/2], scales [n, k/32],
+ * y bf16 [m, n]; k > 0, k % 32 == 0. */
+int dsv4_mxfp4_gemv_bf16(const void* x, int m, const void* packed, const void* scales, int n, int k, void* y,
+                         void* stream);
+
 /* Per-128 FP8 E4M3 activation quantisation with power-of-two scales.
  * Replaces npu_ops.act_quant (npu_ops.py:73-104): `rt` receives the inplace
  * round trip (what act_quant(x, 128, "ue8m0", None, True) writes), `codes` the

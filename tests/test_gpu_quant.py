@@ -1,12 +1,12 @@
-"""GPU parity: MXFP4 dequant, FP8 act_quant round trip and MXFP4 activation quant.
-
-All bit-exact against the oracle (NaN only arises from E8M0 byte 255 and is
-emitted as 0x7FC0 by both)."""
+"""GPU parity: MXFP4 dequant, FP8 act_quant round trip and MXFP4 activation quant,
+all bit-exact against the oracle (NaN only arises from E8M0 byte 255 and is
+emitted as 0x7FC0 by both); and the config-0 dequant + bf16 GEMV, within 1e-2."""
 
 import numpy as np
 import pytest
 import torch
 
+from oracle import moe as M_
 from oracle import mxfp4 as Q
 from dsv4_hip import ops, synth, RULE_CEIL_DIV6, RULE_OCP_FLOOR
 
@@ -114,3 +114,27 @@ def test_mxfp4_quant_random(gpu, rule, name, scale):
 def test_cpu_tensor_is_rejected(gpu):
     with pytest.raises(RuntimeError, match="ROCm device"):
         ops.dequant_mxfp4(torch.zeros(4, 16, dtype=torch.uint8), torch.zeros(4, 1, dtype=torch.uint8))
+
+
+@pytest.mark.parametrize("M", [1, 3, 16])
+def test_mxfp4_gemv_config0(gpu, M):
+    # config 0: bf16 x @ dequant(W)^T against the oracle (fp64 sum of the exact
+    # products, rounded once), tolerance 1e-2 max-relative
+    packed, scales, x0 = synth.dequant_config0()
+    x = x0 if M == 1 else synth.bf16_normal(np.random.default_rng(40 + M), (M, 4096))
+    xb = x.view(torch.int16).numpy().view(np.uint16)
+    y = ops.mxfp4_gemv(x.to(gpu), _u8(packed, gpu), _u8(scales, gpu))
+    torch.cuda.synchronize()
+    got = Q.bf16_bits_to_f32(_bits(y))
+    want = Q.bf16_bits_to_f32(M_.dequant_gemv(xb, packed, scales))
+    assert got.shape == (M, 2048)
+    assert np.abs(got - want).max() <= 1e-2 * np.abs(want).max()
+
+
+def test_mxfp4_gemv_rejects_bad_shapes(gpu):
+    with pytest.raises(ValueError):
+        ops.mxfp4_gemv(torch.zeros(1, 64, dtype=torch.bfloat16, device=gpu),
+                       torch.zeros(8, 16, dtype=torch.uint8, device=gpu), torch.zeros(8, 2, dtype=torch.uint8, device=gpu))
+    with pytest.raises(ops._lib.Dsv4Error, match="at most 16"):
+        ops.mxfp4_gemv(torch.zeros(17, 64, dtype=torch.bfloat16, device=gpu),
+                       torch.zeros(8, 32, dtype=torch.uint8, device=gpu), torch.zeros(8, 2, dtype=torch.uint8, device=gpu))
