@@ -50,7 +50,7 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default="",
-                    help="profile helper: run only 'decode', 'dequant', 'prefill', 'router', 'shared' or 'offload'")
+                    help="profile helper: run only 'decode', 'dequant', 'prefill', 'router', 'routed', 'shared' or 'offload'")
     ap.add_argument("--offload-steps", type=int, default=512, help="decode steps of the expert-offload leg")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy 1 GiB device-to-device (a plain copy of known size for counter calibration)")
@@ -315,6 +315,75 @@ def measure_shared(dev, gen, steps=200, n_sets=8):
             "shared_extra_gbs": shared_bytes / max(t_s - t_r, 1e-9) / 1e9}
 
 
+def measure_routed_layer(dev, gen, steps=200, n_sets=8):
+    """The decode layer with its router (8 tokens, hidden 4096, fp32 gate [256, 4096],
+    sqrt(softplus) scores with a correction bias, top-8, bf16 profile): dsv4_moe_route
+    followed by dsv4_moe_layer_forward, against dsv4_moe_routed_layer_forward, which
+    runs the top-k, the expert layout and the quantisation of x in one launch. Every
+    expert is resident (the whole layer in HBM); each weight set has its own gate.
+    The C entry points are called directly on preallocated buffers, so the host
+    enqueues faster than the GPU runs and the time is the GPU's."""
+    import ctypes
+    from dsv4_hip import _lib, PROFILE_BF16, RULE_OCP_FLOOR
+    lib = _lib.lib()
+    pools, tables = gen_layer_weights(dev, n_sets, gen)
+    rng = np.random.default_rng(41)
+    gates = [torch.from_numpy((rng.standard_normal((E, D)) * 0.03).astype(np.float32)).to(dev) for _ in range(n_sets)]
+    biases = [torch.from_numpy((rng.standard_normal(E) * 0.1).astype(np.float32)).to(dev) for _ in range(n_sets)]
+    xs = [x.to(dev) for x, _, _ in routing_batches(n_sets, 8, 8, 12)]
+    T, K = 8, 8
+    n_ws = ctypes.c_int64(0)
+    lib.dsv4_moe_routed_layer_workspace_bytes(T, K, E, D, I, PROFILE_BF16, 0, ctypes.byref(n_ws))
+    ws = torch.empty(n_ws.value, dtype=torch.uint8, device=dev)
+    n_l = ctypes.c_int64(0)
+    lib.dsv4_moe_layer_workspace_bytes(T, K, E, D, I, PROFILE_BF16, ctypes.byref(n_l))
+    ws_l = torch.empty(n_l.value, dtype=torch.uint8, device=dev)
+    ws_r = torch.empty(max(int(lib.dsv4_moe_route_workspace_bytes(T, D, E)), 4), dtype=torch.uint8, device=dev)
+    out_w = torch.empty(T, K, dtype=torch.float32, device=dev)
+    out_ids = torch.empty(T, K, dtype=torch.int32, device=dev)
+    y = torch.empty(T, D, dtype=torch.bfloat16, device=dev)
+    st = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    sq = _lib.SCORING["sqrtsoftplus"]
+    route_args, layer_args, fused_args = [], [], []
+    for i in range(n_sets):
+        x, g, b, tab = xs[i], gates[i], biases[i], tables[i]
+        route_args.append((P(x), 0, P(g), P(b), None, 0, 0, None, 0, T, D, E, K, sq, 1, 1.5, P(out_w), P(out_ids),
+                           None, P(ws_r), st))
+        layer_args.append((PROFILE_BF16, RULE_OCP_FLOOR, P(x), P(out_ids), 0, P(out_w), T, K, E, D, I, P(tab), 10.0,
+                           P(ws_l), ws_l.numel(), P(y), st))
+        fused_args.append((PROFILE_BF16, RULE_OCP_FLOOR, P(x), T, K, E, D, I, P(g), P(b), None, 0, 0, None, 0, sq, 1,
+                           1.5, P(tab), None, None, None, None, None, None, 10.0, P(out_w), P(out_ids), None, P(ws),
+                           ws.numel(), P(y), st))
+    f_route, f_layer, f_fused = lib.dsv4_moe_route, lib.dsv4_moe_layer_forward, lib.dsv4_moe_routed_layer_forward
+
+    def two_calls(i):
+        if f_route(*route_args[i % n_sets]) or f_layer(*layer_args[i % n_sets]):
+            raise RuntimeError(lib.dsv4_last_error().decode())
+
+    def one_call(i):
+        if f_fused(*fused_args[i % n_sets]):
+            raise RuntimeError(lib.dsv4_last_error().decode())
+
+    res = {}
+    for name, fn in (("route_then_layer", two_calls), ("routed_layer", one_call)):
+        for i in range(20):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            fn(i)
+        e1.record()
+        e1.synchronize()
+        res[f"ms_per_layer_{name}"] = e0.elapsed_time(e1) / steps
+    res["tokens_per_s_routed_layer"] = T / (res["ms_per_layer_routed_layer"] * 1e-3)
+    res["saved_us"] = (res["ms_per_layer_route_then_layer"] - res["ms_per_layer_routed_layer"]) * 1e3
+    del pools, tables
+    torch.cuda.empty_cache()
+    return res
+
+
 def measure_router(dev, iters=200):
     """dsv4_moe_route (gate logits + score + top-8 + weights) at decode and prefill
     token counts: 256 experts, hidden 4096, fp32 gate weight, sqrt(softplus) scores
@@ -372,7 +441,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the expert path shards by expert across GPUs, see DESIGN.md)", file=sys.stderr)
+              "(across GPUs the expert path would shard by expert, with an all-to-all of routed rows per layer)", file=sys.stderr)
         sys.exit(2)
     from dsv4_hip import ops, PROFILE_A4W4, PROFILE_BF16, RULE_OCP_FLOOR
     dev = torch.device("cuda:0")
@@ -451,6 +520,8 @@ def main():
         torch.cuda.empty_cache()
     if not args.no_extra and args.only in ("", "router"):
         extra["router"] = measure_router(dev)
+    if not args.no_extra and args.only in ("", "routed"):
+        extra["decode_routed_layer"] = measure_routed_layer(dev, gen)
     if not args.no_extra and args.only in ("", "shared"):
         extra["decode_with_shared_expert"] = measure_shared(dev, gen)
     if not args.no_extra and args.only in ("", "offload") and args.offload_steps > 0:

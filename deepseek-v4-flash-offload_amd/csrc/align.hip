@@ -17,6 +17,7 @@
 #include "common.h"
 #include "kernels.h"
 #include "quant_dev.h"
+#include "route_dev.h"
 
 namespace {
 
@@ -307,6 +308,31 @@ __global__ __launch_bounds__(NT) void moe_align_quant_kernel(const IdT* __restri
     dsv4::mxfp4_quant_group(x, g, g < n_groups, rule, (uint32_t*)q_codes, (uint8_t*)q_scale, nullptr);
 }
 
+// Decode-sized router + align in the layer's first launch (the router's top-k
+// and moe_align fused, so the routed ids never wait for another launch):
+// workgroup 0's waves each select the top-k of one token at a time
+// (route_topk_token, the router's own per-token code, writing ra.out_ids and
+// ra.out_w), and after a barrier - which also makes those global writes
+// visible to the whole workgroup - the same workgroup aligns them. Workgroups
+// 1.. quantise x as in moe_align_quant_kernel.
+template <int EPL, int NT, int QF>
+__global__ __launch_bounds__(NT) void route_align_quant_kernel(RouteTopkArgs ra, int block_m, int max_blocks,
+                                                               Dsv4AlignOut o, const uint4* __restrict__ x,
+                                                               int64_t n_groups, int rule, void* q_codes,
+                                                               void* q_scale, int n_shared) {
+  if (blockIdx.x == 0) {
+    for (int t = threadIdx.x >> 6; t < ra.T; t += NT / 64) dsv4::route_topk_token<EPL>(ra, t, threadIdx.x & 63);
+    __syncthreads();
+    align_body<int32_t, NT>(ra.out_ids, ra.out_w, ra.T * ra.K, ra.K, ra.E, block_m, max_blocks, o, n_shared);
+    return;
+  }
+  const int64_t g = (int64_t)(blockIdx.x - 1) * NT + threadIdx.x;
+  if (QF == 0)
+    dsv4::fp8_quant_group(x, g, g < n_groups, nullptr, (uint2*)q_codes, nullptr, (uint32_t*)q_scale);
+  else
+    dsv4::mxfp4_quant_group(x, g, g < n_groups, rule, (uint32_t*)q_codes, (uint8_t*)q_scale, nullptr);
+}
+
 }  // namespace
 
 hipError_t launch_moe_align(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K, int E,
@@ -400,5 +426,40 @@ hipError_t launch_moe_align_chunked(const void* topk_ids, int ids_int64, const f
     if (ids_int64) DSV4_SC(long long, 1024); else DSV4_SC(int32_t, 1024);
   }
 #undef DSV4_SC
+  return hipGetLastError();
+}
+
+// 8 waves: one token per wave at decode batch sizes, and E <= 512 experts for
+// the align's one-thread-per-expert layout step.
+hipError_t launch_route_align_quant(const RouteTopkArgs& ra, int block_m, int max_blocks, const Dsv4AlignOut& o,
+                                    const uint16_t* x, int64_t n_elems, int qfmt, int rule, void* q_codes,
+                                    void* q_scale, hipStream_t st, int n_shared) {
+  constexpr int NT = 512;
+  if (ra.E > NT || ra.E <= 0 || (int64_t)ra.T * ra.K > 0x7fffffffLL) return hipErrorInvalidValue;
+  const int E = ra.E;
+  const size_t lds = sizeof(int) * (size_t)((E + 1) + E + E + (E + 1) + (NT / 64) * (E + 1));
+  const int64_t n_groups = n_elems / 8;
+  const int64_t qwg = (n_groups + NT - 1) / NT;
+  if (qwg + 1 > 0x7fffffffLL) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(1 + qwg));
+#define DSV4_RAQ(EPL, QF)                                                                                  \
+  hipLaunchKernelGGL((route_align_quant_kernel<EPL, NT, QF>), grid, dim3(NT), lds, st, ra, block_m, max_blocks, \
+                     o, (const uint4*)x, n_groups, rule, q_codes, q_scale, n_shared)
+#define DSV4_RAQ_E(QF)       \
+  if (E <= 64)               \
+    DSV4_RAQ(1, QF);         \
+  else if (E <= 128)         \
+    DSV4_RAQ(2, QF);         \
+  else if (E <= 256)         \
+    DSV4_RAQ(4, QF);         \
+  else                       \
+    DSV4_RAQ(8, QF)
+  if (qfmt == 0) {
+    DSV4_RAQ_E(0);
+  } else {
+    DSV4_RAQ_E(1);
+  }
+#undef DSV4_RAQ_E
+#undef DSV4_RAQ
   return hipGetLastError();
 }

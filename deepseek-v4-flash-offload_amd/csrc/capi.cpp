@@ -310,7 +310,7 @@ int dsv4_moe_gemm_down(int afmt, const void* a, const void* a_scale, const int32
 // measured to cost far more than the launches they would save. Workspace
 // regions are 256-byte aligned.
 struct LayerWs {
-  int64_t sorted_ids, block_expert, npp, status, xa, xs, h, ha, hs, out, align_scratch, total;
+  int64_t sorted_ids, block_expert, npp, status, xa, xs, h, ha, hs, out, align_scratch, route_part, total;
   int max_blocks;
   int bm;
 };
@@ -320,7 +320,8 @@ struct LayerWs {
 // from there on, where the Zipf-hot experts receive hundreds of rows.
 static int layer_block_m(int64_t R) { return R >= 2048 ? 64 : DSV4_GEMM_BLOCK_M; }
 
-static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool shared = false) {
+static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool shared = false,
+                        bool routed = false) {
   LayerWs w{};
   const int64_t R = (int64_t)T * K;
   const int64_t Rt = R + (shared ? T : 0);  // routed rows, then the shared expert's T rows
@@ -341,16 +342,45 @@ static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool sha
   w.hs = take(Rt * I / 32);
   w.out = take(2 * Rt * D);
   w.align_scratch = R > kAlignSmallRows ? take(align_chunked_scratch_bytes((int)R, E)) : 0;
+  w.route_part = routed ? take(dsv4_moe_route_workspace_bytes(T, D, E)) : -1;  // router partial logits
   w.total = o;
   return w;
 }
 
+// Router arguments of the layer entry that also routes (deepseek_v4.py:118-148).
+struct LayerRoute {
+  const float* gate_w;
+  const float* bias;
+  const void* tid2eid;
+  int tid_is64;
+  int64_t vocab;
+  const void* input_ids;
+  int ids_is64;
+  int scoring;
+  int renorm;
+  float scale;
+  float* out_w;      // [T, K] routing weights (written)
+  int32_t* out_ids;  // [T, K] expert ids (written)
+  int32_t* status;   // nullable: bad input ids / table entries
+};
+
+// Batches up to this many tokens route inside the layer's first launch (one
+// token per wave of the align workgroup); larger ones route in the router's
+// own two launches first.
+constexpr int kFusedRouteTokens = 16;
+
 // The routed layer, and with `shared` the shared expert as one more group of
-// T rows (bf16 profile only; checked by the caller).
+// T rows (bf16 profile only; checked by the caller). With `route` the layer
+// first routes x itself: topk_ids / topk_w are then the route's outputs.
 static int layer_forward(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
                          const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
                          const Dsv4ExpertPtrs* shared, float swiglu_limit, void* workspace, int64_t workspace_bytes,
-                         void* y, void* stream) {
+                         void* y, void* stream, const LayerRoute* route = nullptr) {
+  if (route) {
+    topk_ids = route->out_ids;
+    ids_int64 = 0;
+    topk_w = route->out_w;
+  }
   REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4, DSV4_ERR_UNSUPPORTED,
           "layer: unknown profile %d", profile);
   REQUIRE(T >= 0 && K > 0 && K <= DSV4_MAX_TOPK, DSV4_ERR_SHAPE, "layer: bad T=%d K=%d", T, K);
@@ -358,7 +388,7 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
           "layer: D=%d and I=%d must be multiples of 512", D, I);
   if (T == 0) return DSV4_OK;
   REQUIRE(x && topk_ids && topk_w && expert_table && workspace && y, DSV4_ERR_NULL, "layer: null pointer");
-  const LayerWs w = layer_ws(T, K, E, D, I, profile, shared != nullptr);
+  const LayerWs w = layer_ws(T, K, E, D, I, profile, shared != nullptr, route != nullptr);
   REQUIRE(workspace_bytes >= w.total, DSV4_ERR_SHAPE, "layer: workspace %lld < %lld bytes",
           (long long)workspace_bytes, (long long)w.total);
   REQUIRE(aligned(workspace, 256), DSV4_ERR_SHAPE, "layer: workspace not 256-byte aligned");
@@ -382,7 +412,29 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
   // routing layout and the activation quantisation of x share one launch
   Dsv4AlignOut ao{sorted_ids, block_expert, npp, nullptr, nullptr, nullptr, nullptr, nullptr,
                   nullptr,    nullptr,      nullptr, nullptr, status};
-  int rc = hip_status(
+  int rc = DSV4_OK;
+  bool aligned_already = false;
+  if (route) {
+    int S = 1;
+    float* part = (float*)(base + w.route_part);
+    rc = hip_status(launch_route_logits(x, 0, route->gate_w, T, D, E, part, &S, (hipStream_t)stream),
+                    "route logits launch");
+    if (rc) return rc;
+    const RouteTopkArgs ra{part, S, T, E, K, route->scoring, route->bias, route->tid2eid, route->tid_is64,
+                           route->input_ids, route->ids_is64, route->vocab, route->renorm, route->scale,
+                           route->out_w, route->out_ids, route->status};
+    if (T <= kFusedRouteTokens && R <= kAlignSmallRows) {  // top-k, align and x quantisation in one launch
+      rc = hip_status(launch_route_align_quant(ra, bm, w.max_blocks, ao, (const uint16_t*)x, (int64_t)T * D,
+                                               fp8 ? 0 : 1, scale_rule, base + w.xa, base + w.xs,
+                                               (hipStream_t)stream, n_sh),
+                      "route+align+quant launch");
+      aligned_already = true;
+    } else {
+      rc = hip_status(launch_route_topk(ra, (hipStream_t)stream), "route top-k launch");
+    }
+    if (rc) return rc;
+  }
+  if (!aligned_already) rc = hip_status(
       R > kAlignSmallRows
           ? launch_moe_align_chunked(topk_ids, ids_int64, nullptr, R, K, E, bm, w.max_blocks, ao, (const uint16_t*)x,
                                      (int64_t)T * D, fp8 ? 0 : 1, scale_rule, base + w.xa, base + w.xs,
@@ -510,6 +562,55 @@ int dsv4_moe_layer_forward_shared(const void* x, const void* topk_ids, int ids_i
                           (const uint8_t*)sw2s, (const uint8_t*)sw3, (const uint8_t*)sw3s};
   return layer_forward(DSV4_PROFILE_BF16, DSV4_RULE_OCP_FLOOR, x, topk_ids, ids_int64, topk_w, T, K, E, D, I,
                        expert_table, &sh, swiglu_limit, workspace, workspace_bytes, y, stream);
+}
+
+int dsv4_moe_routed_layer_workspace_bytes(int T, int K, int E, int D, int I, int profile, int with_shared,
+                                          int64_t* bytes) {
+  REQUIRE(bytes, DSV4_ERR_NULL, "workspace: null output");
+  REQUIRE(T >= 0 && K > 0 && E > 0 && D > 0 && I > 0, DSV4_ERR_SHAPE, "workspace: bad sizes");
+  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4, DSV4_ERR_UNSUPPORTED,
+          "workspace: unknown profile %d", profile);
+  *bytes = layer_ws(T, K, E, D, I, profile, with_shared != 0, true).total;
+  return DSV4_OK;
+}
+
+int dsv4_moe_routed_layer_forward(int profile, int scale_rule, const void* x, int T, int K, int E, int D, int I,
+                                  const float* gate_w, const float* bias, const void* tid2eid, int tid2eid_int64,
+                                  int64_t vocab, const void* input_ids, int input_ids_int64, int scoring,
+                                  int renormalize, float routed_scale, const void* expert_table, const void* sw1,
+                                  const void* sw1s, const void* sw3, const void* sw3s, const void* sw2,
+                                  const void* sw2s, float swiglu_limit, float* topk_w_out, int32_t* topk_ids_out,
+                                  int32_t* route_status, void* workspace, int64_t workspace_bytes, void* y,
+                                  void* stream) {
+  REQUIRE(T >= 0, DSV4_ERR_SHAPE, "routed layer: negative T");
+  REQUIRE(E >= 16 && E <= 512 && E % 16 == 0, DSV4_ERR_UNSUPPORTED,
+          "routed layer: %d experts unsupported (multiple of 16 in 16..512)", E);
+  REQUIRE(K >= 1 && K <= E && K <= 64 && K <= DSV4_MAX_TOPK, DSV4_ERR_UNSUPPORTED,
+          "routed layer: top-k %d outside 1..min(E, 64, %d)", K, DSV4_MAX_TOPK);
+  REQUIRE(scoring >= 0 && scoring <= 2, DSV4_ERR_UNSUPPORTED,
+          "routed layer: scoring %d unknown (0 softmax, 1 sigmoid, 2 sqrtsoftplus)", scoring);
+  if (T == 0) return DSV4_OK;
+  REQUIRE(gate_w && topk_w_out && topk_ids_out, DSV4_ERR_NULL, "routed layer: null router pointer");
+  REQUIRE(aligned(gate_w, 16), DSV4_ERR_SHAPE, "routed layer: gate weight not 16-byte aligned");
+  if (tid2eid) {
+    REQUIRE(input_ids, DSV4_ERR_NULL, "routed layer: hash-layer routing needs input_ids");
+    REQUIRE(vocab > 0, DSV4_ERR_SHAPE, "routed layer: tid2eid needs vocab > 0");
+  }
+  const bool has_shared = sw1 || sw1s || sw3 || sw3s || sw2 || sw2s;
+  Dsv4ExpertPtrs sh{};
+  if (has_shared) {
+    REQUIRE(profile == DSV4_PROFILE_BF16, DSV4_ERR_UNSUPPORTED, "routed layer: the shared expert needs the bf16 profile");
+    REQUIRE(sw1 && sw1s && sw3 && sw3s && sw2 && sw2s, DSV4_ERR_NULL, "routed layer: null shared-expert pointer");
+    REQUIRE(aligned(sw1, 16) && aligned(sw3, 16) && aligned(sw2, 16) && aligned(sw1s, 4) && aligned(sw3s, 4) &&
+                aligned(sw2s, 4),
+            DSV4_ERR_SHAPE, "routed layer: misaligned shared-expert weights");
+    sh = Dsv4ExpertPtrs{(const uint8_t*)sw1, (const uint8_t*)sw1s, (const uint8_t*)sw2,
+                        (const uint8_t*)sw2s, (const uint8_t*)sw3, (const uint8_t*)sw3s};
+  }
+  const LayerRoute rt{gate_w, bias, tid2eid, tid2eid_int64, vocab, input_ids, input_ids_int64, scoring,
+                      renormalize, routed_scale, topk_w_out, topk_ids_out, route_status};
+  return layer_forward(profile, scale_rule, x, nullptr, 0, nullptr, T, K, E, D, I, expert_table,
+                       has_shared ? &sh : nullptr, swiglu_limit, workspace, workspace_bytes, y, stream, &rt);
 }
 
 }  // extern "C"

@@ -114,9 +114,37 @@ hipError_t launch_moe_gemm_down(const Dsv4GemmArgs& a, hipStream_t st);
 bool moe_gemm_supported_kdim(int kdim);  // reduction lengths with a compiled kernel (512..8192, powers of two)
 bool moe_gemm_supported_block_m(int bm);  // 16 (decode kernel), 64 or 128 (tiled kernel)
 
+// Router top-k of one layer (per-token arguments of route_topk_token).
+struct RouteTopkArgs {
+  const float* part;  // [S, T, E] partial logits (K chunks)
+  int S, T, E, K, scoring;
+  const float* bias;
+  const void* tid2eid;
+  int tid_is64;
+  const void* input_ids;
+  int ids_is64;
+  int64_t vocab;
+  int renorm;
+  float scale;
+  float* out_w;      // [T, K]
+  int32_t* out_ids;  // [T, K]
+  int32_t* status;
+};
+
 // Router: partial logits [S, T, E] in `part`, then scores / top-k / weights.
 int route_split_k(int T, int D, int E);
 hipError_t launch_moe_route(const void* x, int x_f32, const float* gate_w, int T, int D, int E, int K, int scoring,
                             const float* bias, const void* tid2eid, int tid_is64, const void* input_ids,
                             int ids_is64, int64_t vocab, int renorm, float scale, float* out_w,
                             int32_t* out_ids, int32_t* status, float* part, hipStream_t st);
+// The two halves of launch_moe_route: the partial logits (returns the K split S
+// through *S), and the per-token top-k over them.
+hipError_t launch_route_logits(const void* x, int x_f32, const float* gate_w, int T, int D, int E, float* part,
+                               int* S, hipStream_t st);
+hipError_t launch_route_topk(const RouteTopkArgs& ra, hipStream_t st);
+// Decode-sized routing straight into the layer's first launch: workgroup 0
+// selects every token's top-k (ra.out_ids / ra.out_w) and then aligns them,
+// workgroups 1.. quantise x (as launch_moe_align_quant; R = T * K <= 2048).
+hipError_t launch_route_align_quant(const RouteTopkArgs& ra, int block_m, int max_blocks, const Dsv4AlignOut& o,
+                                    const uint16_t* x, int64_t n_elems, int qfmt, int rule, void* q_codes,
+                                    void* q_scale, hipStream_t st, int n_shared = 0);

@@ -59,6 +59,10 @@ SIGNATURES = {
     "dsv4_moe_layer_forward_shared": (_i32, [_c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32, _c_p] + [_c_p] * 6
                                       + [_f32, _c_p, _i64, _c_p, _c_p]),
     "dsv4_expand_block_scales": (_i32, [_c_p, _i64, _i64, _c_p, _c_p]),
+    "dsv4_moe_routed_layer_workspace_bytes": (_i32, [_i32] * 7 + [ctypes.POINTER(_i64)]),
+    "dsv4_moe_routed_layer_forward": (_i32, [_i32, _i32, _c_p] + [_i32] * 5 + [_c_p, _c_p, _c_p, _i32, _i64, _c_p, _i32,
+                                             _i32, _i32, _f32, _c_p] + [_c_p] * 6
+                                      + [_f32, _c_p, _c_p, _c_p, _c_p, _i64, _c_p, _c_p]),
     # slot cache
     "dsv4_lru_create": (_i32, [_i32, ctypes.POINTER(_c_p)]),
     "dsv4_lru_destroy": (_i32, [_c_p]),

@@ -403,3 +403,54 @@ class LayerRunner:
         call("dsv4_moe_layer_forward", profile, rule, _p(x), _p(ids), i64, _p(w), T, K, self.E, D, self.I,
              _p(table), lim, _p(ws), ws.numel(), _p(y), _stream(x))
         return y
+
+    def forward_routed(self, x, gate_w, topk, table, scoring="sqrtsoftplus", bias=None, renormalize=True,
+                       scale=1.5, tid2eid=None, input_ids=None, status=None, profile=_lib.PROFILE_BF16,
+                       rule=_lib.RULE_OCP_FLOOR, swiglu_limit=10.0, out=None, shared=None):
+        """Router + routed layer in one C call (``dsv4_moe_routed_layer_forward``):
+        ``_routed(hs, input_ids)`` of ``deepseek_v4.py:150-245`` with its ``_route``
+        (``:118-148``), plus the shared expert when ``shared`` is given. Returns
+        ``(y bf16 [T, D], weights fp32 [T, K], ids int32 [T, K])``, the same as
+        ``route`` followed by ``forward`` on its ids. Arguments as in ``route``;
+        x must be bf16."""
+        _dev(x, "routed_layer_forward")
+        if x.dtype != torch.bfloat16 or not x.is_contiguous():
+            raise TypeError("routed_layer_forward: contiguous bf16 activations required")
+        if scoring not in _lib.SCORING:
+            raise ValueError(f"routed_layer_forward: unknown scoring function {scoring!r}")
+        T, D = x.shape
+        w = gate_w.to(torch.float32).contiguous()
+        if w.dim() != 2 or w.shape != (self.E, D):
+            raise ValueError(f"routed_layer_forward: gate weight {tuple(w.shape)} is not [{self.E}, {D}]")
+        b = None if bias is None else bias.to(torch.float32).contiguous()
+        tab, ids_in, vocab = None, None, 0
+        if tid2eid is not None:
+            if input_ids is None:
+                raise RuntimeError("hash-layer routing needs input_ids")
+            tab = tid2eid.contiguous()
+            if tab.dtype not in (torch.int32, torch.int64) or tab.dim() != 2 or tab.shape[1] != topk:
+                raise ValueError("routed_layer_forward: tid2eid must be int32/int64 [vocab, topk]")
+            ids_in = input_ids.reshape(-1).contiguous()
+            if ids_in.dtype not in (torch.int32, torch.int64):
+                ids_in = ids_in.to(torch.int64)
+            if ids_in.numel() != T:
+                raise ValueError(f"routed_layer_forward: {ids_in.numel()} input ids for {T} tokens")
+            vocab = tab.shape[0]
+        if shared is not None and profile != _lib.PROFILE_BF16:
+            raise ValueError("routed_layer_forward: the shared expert is fused in the bf16 profile only")
+        n = ctypes.c_int64(0)
+        call("dsv4_moe_routed_layer_workspace_bytes", T, topk, self.E, D, self.I, profile,
+             1 if shared is not None else 0, ctypes.byref(n))
+        if self._ws is None or self._ws.numel() < n.value:
+            self._ws = torch.empty(max(n.value, 256), dtype=torch.uint8, device=self.device)
+        ws = self._ws
+        y = out if out is not None else torch.empty((T, D), dtype=torch.bfloat16, device=x.device)
+        out_w = torch.empty(T, topk, dtype=torch.float32, device=x.device)
+        out_ids = torch.empty(T, topk, dtype=torch.int32, device=x.device)
+        sh = [None] * 6 if shared is None else [shared[k] for k in ("w1", "w1s", "w3", "w3s", "w2", "w2s")]
+        call("dsv4_moe_routed_layer_forward", profile, rule, _p(x), T, topk, self.E, D, self.I, _p(w), _p(b),
+             _p(tab), 1 if tab is not None and tab.dtype == torch.int64 else 0, vocab, _p(ids_in),
+             1 if ids_in is not None and ids_in.dtype == torch.int64 else 0, _lib.SCORING[scoring],
+             1 if renormalize else 0, float(scale), _p(table), *[_p(t) for t in sh], float(swiglu_limit or 0.0),
+             _p(out_w), _p(out_ids), _p(status), _p(ws), ws.numel(), _p(y), _stream(x))
+        return y, out_w, out_ids

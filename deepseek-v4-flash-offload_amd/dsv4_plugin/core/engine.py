@@ -123,6 +123,11 @@ class ExpertOffloadEngine:
     def prefetch(self, layer: int, expert_ids):
         return self.bank.prefetch(layer, expert_ids)
 
+    def resident_table(self, layer: int, n_experts: int):
+        """Pointer table of every expert of ``layer`` while all registered experts fit
+        the slot cache (None otherwise); see ``ExpertBank.resident_table``."""
+        return self.bank.resident_table(layer, n_experts)
+
     def stats(self):
         s = self.bank.stats()
         s["captured"] = self.captured

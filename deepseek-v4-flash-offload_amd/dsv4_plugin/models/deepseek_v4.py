@@ -66,6 +66,13 @@ _FUSE_SHARED = os.environ.get("DSV4_FUSE_SHARED", "0") == "1"
 # GEMMs, so the copies overlap its compute. Read at call time; env
 # DSV4_PREFETCH_NEXT=1. Layers register themselves by index.
 _PREFETCH_NEXT = os.environ.get("DSV4_PREFETCH_NEXT", "0") == "1"
+
+# When every expert of every layer fits the slot cache (on a 288 GB MI355X the
+# whole routed expert set can), route and run the experts in one device call:
+# top-k, expert layout and x quantisation share a launch and the routed ids
+# never go to the host. The result equals _route + _run_experts bit for bit.
+# Read at call time; env DSV4_FUSED_ROUTE=0 turns it off.
+_FUSED_ROUTE = os.environ.get("DSV4_FUSED_ROUTE", "1") == "1"
 _LAYERS = weakref.WeakValueDictionary()
 
 _BASE = v4.DeepseekV4MoE if (v4 is not None and hasattr(v4, "DeepseekV4MoE")) else nn.Module
@@ -240,9 +247,35 @@ class OffloadDeepseekV4MoE(_BASE):
         profile when the module toggle ``_MXFP4_GMM`` is set (``:199-245``).
         ``shared`` (a prepared FP8 shared expert, bf16 profile) adds the shared
         expert's output computed in the same launches."""
-        weights, indices = self._route(hs, input_ids)
         profile = _lib.PROFILE_A4W4 if _MXFP4_GMM else _lib.PROFILE_BF16
+        if hs.is_cuda and _FUSED_ROUTE and not _PREFETCH_NEXT:
+            y = self._routed_resident(hs, input_ids, profile, shared)
+            if y is not None:
+                return y
+        weights, indices = self._route(hs, input_ids)
         return self._run_experts(hs, weights, indices, profile, input_ids, shared)
+
+    def _routed_resident(self, hs, input_ids, profile, shared):
+        """Router and experts in one call (``dsv4_moe_routed_layer_forward``) when the
+        engine keeps every expert of this layer resident; None when it cannot."""
+        eng = self.engine
+        T, D = hs.shape
+        if T == 0 or not hasattr(eng, "resident_table"):
+            return None
+        if self.hash and input_ids is None:
+            raise RuntimeError("hash-layer routing needs input_ids (forward_context.input_ids is missing)")
+        table = eng.resident_table(self.layer_idx, self.n_routed_experts)
+        if table is None:
+            return None
+        x = hs if (hs.dtype == torch.bfloat16 and hs.is_contiguous()) else hs.to(torch.bfloat16).contiguous()
+        inter = eng.bank._layout.shapes["w1p"][0]
+        limit = self.swiglu_limit if (self.swiglu_limit and self.swiglu_limit > 0) else 0.0
+        y, _, _ = _runner(hs.device, self.n_routed_experts, D, inter).forward_routed(
+            x, self.gate.weight, self.topk, table, self.scoring_func,
+            bias=None if self.hash else self.gate.e_score_correction_bias, renormalize=bool(self.renormalize),
+            scale=float(self.routed_scaling_factor), tid2eid=self.gate.tid2eid if self.hash else None,
+            input_ids=input_ids, profile=profile, rule=_RULES[_MX_RULE], swiglu_limit=limit, shared=shared)
+        return y.type_as(hs)
 
     def _fused_shared(self, hs):
         if not (_FUSE_SHARED and not _MXFP4_GMM and hs.is_cuda and hasattr(self.engine, "get_shared")):

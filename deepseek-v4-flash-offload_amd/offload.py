@@ -64,6 +64,7 @@ class ExpertBank:
         self.packed_capacity = int(os.environ.get("DSV4_PACKED_SLOTS", str(4 * self.capacity)))
         self._slots = None
         self._layout = None
+        self._resident = {}        # layer -> (registered count, full pointer table)
 
     # -- host bank --------------------------------------------------------
     def _ensure_slots(self, tensors):
@@ -147,6 +148,31 @@ class ExpertBank:
         slots, n_miss = self._slots.acquire(int(layer), eids)
         return self._slots.table(eids, slots, n_experts), n_miss
 
+    def resident_table(self, layer, n_experts):
+        """Device pointer table [E, 6] of every registered expert of ``layer``, or
+        None. Only when the packed slot cache can hold every registered expert of
+        every layer at once: then no acquire can evict one, the table stays valid,
+        and the routed ids never need to reach the host. The first call per layer
+        copies its missing experts in; the table is rebuilt when more experts are
+        registered. (Lookups through this table are not counted as hits.)"""
+        if self.device.type != "cuda" or self._slots is None:
+            return None
+        n_reg = len(self._slots.keys_registered)
+        if self.packed_capacity < n_reg:
+            return None
+        layer = int(layer)
+        hit = self._resident.get(layer)
+        if hit is not None and hit[0] == n_reg:
+            return hit[1]
+        eids = np.array(sorted(e for (lay, e) in self._slots.keys_registered if lay == layer and 0 <= e < n_experts),
+                        dtype=np.int32)
+        if eids.size == 0:
+            return None
+        slots, _ = self._slots.acquire(layer, eids)
+        tab = self._slots.table(eids, slots, n_experts)
+        self._resident[layer] = (n_reg, tab)
+        return tab
+
     def prefetch(self, layer, expert_ids):
         """Start side-stream copies of the non-resident experts of a coming layer."""
         self._need_gpu("prefetch")
@@ -154,6 +180,7 @@ class ExpertBank:
 
     def invalidate(self):
         self._cache.clear()
+        self._resident.clear()
         if self._slots is not None:
             self._slots.invalidate()
 

@@ -220,6 +220,30 @@ int dsv4_moe_layer_forward_shared(const void* x, const void* topk_ids, int ids_i
                                   const void* sw2s, float swiglu_limit, void* workspace, int64_t workspace_bytes,
                                   void* y, void* stream);
 
+/* The routed layer with its router: OffloadDeepseekV4MoE._routed(hs, input_ids)
+ * (deepseek_v4.py:150-245) including its _route call (deepseek_v4.py:118-148),
+ * and, with the six shared-expert pointers set (all null = none; bf16 profile
+ * only), forward's `+ shared_experts(hs)` as in dsv4_moe_layer_forward_shared.
+ * Routing arguments and outputs are those of dsv4_moe_route (x bf16 only);
+ * topk_w_out / topk_ids_out receive the routing [T, K] the layer used. Up to 16
+ * tokens, the router's top-k, the expert layout (moe_align) and the
+ * quantisation of x run in one launch after the logits (the routed ids never
+ * wait for a launch boundary); larger batches route in the router's two
+ * launches first. The outputs equal dsv4_moe_route followed by
+ * dsv4_moe_layer_forward(_shared) on its ids, bit for bit.
+ * workspace: dsv4_moe_routed_layer_workspace_bytes(T, K, E, D, I, profile,
+ * with_shared) bytes. */
+int dsv4_moe_routed_layer_workspace_bytes(int T, int K, int E, int D, int I, int profile, int with_shared,
+                                          int64_t* bytes);
+int dsv4_moe_routed_layer_forward(int profile, int scale_rule, const void* x, int T, int K, int E, int D, int I,
+                                  const float* gate_w, const float* bias, const void* tid2eid, int tid2eid_int64,
+                                  int64_t vocab, const void* input_ids, int input_ids_int64, int scoring,
+                                  int renormalize, float routed_scale, const void* expert_table, const void* sw1,
+                                  const void* sw1s, const void* sw3, const void* sw3s, const void* sw2,
+                                  const void* sw2s, float swiglu_limit, float* topk_w_out, int32_t* topk_ids_out,
+                                  int32_t* route_status, void* workspace, int64_t workspace_bytes, void* y,
+                                  void* stream);
+
 /* out[n][j] = block_scales[n / 128][j / 4] for n < n_rows, j < k/32: the
  * 128x128 block scales of an FP8 weight [n_rows, k] (npu_ops.py:161-167,
  * dequant_fp8_weight) repeated per 32 along K, the layout the grouped GEMMs

@@ -408,3 +408,36 @@ def test_forward_fuses_the_captured_shared_expert(gpu, monkeypatch):
     assert rel(Q.bf16_bits_to_f32(_bits(y_r)), Q.bf16_bits_to_f32(want_r)) <= 1e-2
     assert rel(Q.bf16_bits_to_f32(_bits(y)), Q.bf16_bits_to_f32(want)) <= 1e-2
     assert engine.get_shared(layer, gpu) is engine.get_shared(layer, gpu)   # prepared once per device
+
+
+@pytest.mark.parametrize("is_hash", [False, True])
+def test_forward_routes_inside_the_layer_when_every_expert_is_resident(gpu, monkeypatch, is_hash):
+    # 64 packed slots >= 32 registered experts: the router, the expert layout and the
+    # experts run in one call (dsv4_moe_routed_layer_forward) with no host sync on the
+    # ids; the output equals _route + _run_experts bit for bit
+    E, K, D, I, T, layer = 32, 6, 1024, 512, 8, 3
+    monkeypatch.setenv("DSV4_PACKED_SLOTS", "64")
+    engine = ExpertOffloadEngine(slot_capacity=16, device="cuda:0")
+    for e in range(E):
+        h = synth.expert_weights(e, D, I)
+        for w in ("w1", "w2", "w3"):
+            engine.capture(f"layers.{layer}.ffn.experts.{e}.{w}.weight", torch.from_numpy(h[w + "p"]).view(torch.int8))
+            engine.capture(f"layers.{layer}.ffn.experts.{e}.{w}.scale",
+                           torch.from_numpy(h[w + "s"]).view(torch.float8_e8m0fnu))
+    m = _make_plugin(engine, E, K, layer, is_hash, D)
+    x = (synth.bf16_normal(np.random.default_rng(9), (T, D)).float() * 0.5).to(torch.bfloat16).to(gpu)
+    ids = torch.randint(0, 100, (T,), generator=torch.Generator().manual_seed(4)).to(gpu)
+    monkeypatch.setattr(mod, "_FUSED_ROUTE", False)
+    y_ref = m.forward(x, ids)
+    assert layer not in engine.bank._resident
+    monkeypatch.setattr(mod, "_FUSED_ROUTE", True)
+    y = m.forward(x, ids)
+    torch.cuda.synchronize()
+    assert layer in engine.bank._resident          # the fused path ran
+    assert np.array_equal(_bits(y), _bits(y_ref))
+    # the slot cache can no longer hold every registered expert: back to route + acquire
+    engine.bank.packed_capacity = 16
+    assert engine.resident_table(layer, E) is None
+    y2 = m.forward(x, ids)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(y2), _bits(y_ref))

@@ -190,3 +190,9 @@ def test_tee_keeps_a_copy_of_the_shared_expert():
     assert sorted(engine._shared) == [1, 2] and sorted(engine._shared[1]) == ["w1", "w1s", "w2", "w2s", "w3", "w3s"]
     assert int(engine._shared[2]["w3s"][0, 0]) == names.index("model.layers.2.ffn.shared_experts.w3.scale")
     assert engine.get_shared(5, "cpu") is None      # nothing captured for layer 5
+
+
+def test_resident_table_needs_a_device_bank():
+    # the router-in-layer path needs every expert on the device; a host bank never offers it
+    bank = ExpertBank(capacity=4, device="cpu")
+    assert bank.resident_table(0, 8) is None
