@@ -52,13 +52,20 @@ def parse():
     ap.add_argument("--only", default="",
                     help="profile helper: run only 'decode', 'dequant', 'prefill', 'router', 'routed', 'shared' or 'offload'")
     ap.add_argument("--offload-steps", type=int, default=512, help="decode steps of the expert-offload leg")
+    ap.add_argument("--weight-layout", choices=("tiled", "checkpoint"), default="tiled",
+                    help="packed expert weights in HBM: the MFMA-tiled layout (default) or the checkpoint layout")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first copy 1 GiB device-to-device (a plain copy of known size for counter calibration)")
     return ap.parse_args()
 
 
+WEIGHT_LAYOUT = "tiled"
+
+
 def gen_layer_weights(dev, n_layers, gen):
-    """Per layer: one contiguous [E, EXPERT_BYTES] pool + its pointer table."""
+    """Per layer: one contiguous [E, EXPERT_BYTES] pool + its pointer table. The
+    packed fields are random bytes, read in the layout WEIGHT_LAYOUT names (the
+    MFMA-tiled one by default: what the slot cache holds)."""
     from dsv4_hip import ops
     pools, tables = [], []
     offs = {}
@@ -74,7 +81,7 @@ def gen_layer_weights(dev, n_layers, gen):
             pool[:, a:a + n] = torch.randint(117, 128, (E, n), dtype=torch.uint8, device=dev, generator=gen)
         experts = {e: {k: pool[e, a:a + n] for k, (a, n) in offs.items()} for e in range(E)}
         pools.append(pool)
-        tables.append(ops.expert_table(experts, E, dev))
+        tables.append(ops.expert_table(experts, E, dev, tiled=WEIGHT_LAYOUT == "tiled"))
     return pools, tables
 
 
@@ -438,7 +445,9 @@ def cpu_baseline(sample_steps=2, threads=None, min_seconds=10.0):
 
 
 def main():
+    global WEIGHT_LAYOUT
     args = parse()
+    WEIGHT_LAYOUT = args.weight_layout
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(across GPUs the expert path would shard by expert, with an all-to-all of routed rows per layer)", file=sys.stderr)
@@ -481,7 +490,7 @@ def main():
             "config": {"workload": "bf16-profile MoE decode layer: 8 tokens, 256 experts, top-8 Zipf(1.1), "
                                    "hidden 4096, inter 2048, MXFP4 experts resident in HBM",
                        "tokens": T, "topk": K, "experts": E, "hidden": D, "inter": I,
-                       "weight_sets_cycled": args.layers},
+                       "weight_sets_cycled": args.layers, "weight_layout": WEIGHT_LAYOUT},
             "roofline": {"bound": "hbm", "kernel": "moe_gemm_kernel<E4M3, gate/up>", "achieved": ach,
                          "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": ach / HBM_PEAK_GBS, "traffic": traffic,
                          "traffic_source": "profiles/moe_gemm_decode_bf16_traffic.json" if traffic else None,

@@ -62,6 +62,42 @@ int dsv4_mxfp4_dequant_bf16(const void* packed, const void* scales, void* out, i
                     "dequant launch");
 }
 
+int dsv4_mxfp4_tile_weights(const void* src, void* dst, int64_t n_rows, int64_t k, int inverse, void* stream) {
+  REQUIRE(n_rows >= 0 && k >= 0, DSV4_ERR_SHAPE, "tile weights: negative size");
+  REQUIRE(n_rows % 16 == 0 && k % 256 == 0, DSV4_ERR_SHAPE,
+          "tile weights: [%lld, %lld] needs rows %% 16 == 0 and K %% 256 == 0", (long long)n_rows, (long long)k);
+  REQUIRE(inverse == 0 || inverse == 1, DSV4_ERR_UNSUPPORTED, "tile weights: inverse must be 0 or 1");
+  if (n_rows == 0 || k == 0) return DSV4_OK;
+  REQUIRE(src && dst, DSV4_ERR_NULL, "tile weights: null pointer");
+  REQUIRE(aligned(src, 16) && aligned(dst, 16), DSV4_ERR_SHAPE, "tile weights: buffers must be 16-byte aligned");
+  const int64_t bytes = n_rows * (k / 2);
+  const uintptr_t s0 = (uintptr_t)src, d0 = (uintptr_t)dst;
+  REQUIRE(s0 + bytes <= d0 || d0 + bytes <= s0, DSV4_ERR_SHAPE, "tile weights: src and dst overlap");
+  return hip_status(launch_mxfp4_tile((const uint8_t*)src, (uint8_t*)dst, n_rows, k, inverse, (hipStream_t)stream),
+                    "tile weights launch");
+}
+
+int dsv4_mxfp4_tile_host(const void* src, void* dst, int64_t n_rows, int64_t k) {
+  REQUIRE(n_rows >= 0 && k >= 0, DSV4_ERR_SHAPE, "tile weights (host): negative size");
+  REQUIRE(n_rows % 16 == 0 && k % 256 == 0, DSV4_ERR_SHAPE,
+          "tile weights (host): [%lld, %lld] needs rows %% 16 == 0 and K %% 256 == 0", (long long)n_rows,
+          (long long)k);
+  if (n_rows == 0 || k == 0) return DSV4_OK;
+  REQUIRE(src && dst, DSV4_ERR_NULL, "tile weights (host): null pointer");
+  const uint8_t* s = (const uint8_t*)src;
+  uint8_t* d = (uint8_t*)dst;
+  const int64_t row_bytes = k / 2, nst = k / 256;
+  REQUIRE(s + n_rows * row_bytes <= d || d + n_rows * row_bytes <= s, DSV4_ERR_SHAPE,
+          "tile weights (host): src and dst overlap");
+  for (int64_t nt = 0; nt < n_rows / 16; ++nt)  // destination order: tile, stage, MFMA, lane
+    for (int64_t j = 0; j < nst; ++j)
+      for (int ji = 0; ji < 2; ++ji)
+        for (int g = 0; g < 4; ++g)
+          for (int r = 0; r < 16; ++r, d += 16)
+            memcpy(d, s + (16 * nt + r) * row_bytes + 128 * j + 32 * g + 16 * ji, 16);
+  return DSV4_OK;
+}
+
 int dsv4_mxfp4_gemv_bf16(const void* x, int m, const void* packed, const void* scales, int n, int k, void* y,
                          void* stream) {
   REQUIRE(m >= 0 && n >= 0 && k >= 0, DSV4_ERR_SHAPE, "gemv: negative size");

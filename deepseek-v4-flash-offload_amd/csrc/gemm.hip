@@ -177,8 +177,30 @@ DSV4_DEV void load_a(AStage<AFMT>& a, const uint8_t* abase, const uint8_t* asbas
   if constexpr (SCALES) a.s = ld_u16(asbase + j * 8 + 2 * g);
 }
 
+// E2M1 weight layouts: the lane's chunk for MFMA ji of stage j is at
+// bt + j * stage_stride + ji * mfma_stride, bt being the lane's chunk of stage 0.
+struct BLayout {
+  int64_t stage_stride;  // checkpoint [N, K/2]: 128; MFMA-tiled: 2048
+  int mfma_stride;       // checkpoint: 16; MFMA-tiled: 1024
+};
+// An expert table entry marks a packed weight field in the MFMA-tiled layout
+// (mxfp4_tile_kernel) by bit 0 of its pointer (the fields are 16-byte aligned).
+DSV4_DEV bool tiled_ptr(const uint8_t* p) { return ((uintptr_t)p & 1u) != 0; }
+DSV4_DEV const uint8_t* untag(const uint8_t* p) { return (const uint8_t*)((uintptr_t)p & ~(uintptr_t)1); }
+// The lane's stage-0 chunk of weight row `row` (16-row tile row / 16) and the strides.
+DSV4_DEV const uint8_t* b_lane_base(const uint8_t* w, int64_t row, int64_t row_bytes, int nst, int lane,
+                                    BLayout& lay) {
+  if (tiled_ptr(w)) {
+    lay = BLayout{2048, 1024};
+    return untag(w) + (row >> 4) * (int64_t)nst * 2048 + 16 * lane;
+  }
+  lay = BLayout{128, 16};
+  return w + row * row_bytes + 32 * (lane >> 4);
+}
+
 template <bool SCALES = true, bool B8 = false>
-DSV4_DEV void load_b(BStageT<B8>& b, const uint8_t* const* bt, const uint8_t* const* bst, int j, int g) {
+DSV4_DEV void load_b(BStageT<B8>& b, const uint8_t* const* bt, const uint8_t* const* bst, int j, int g,
+                     const BLayout& lay = BLayout{128, 16}) {
 #pragma unroll
   for (int t = 0; t < BStageT<B8>::NTB; ++t) {
     if constexpr (B8) {  // E4M3 rows: the E4M3 A layout (two 16-byte halves per MFMA)
@@ -190,9 +212,9 @@ DSV4_DEV void load_b(BStageT<B8>& b, const uint8_t* const* bt, const uint8_t* co
         b.d[t][ji] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       }
     } else {
-      const uint8_t* p = bt[t] + (int64_t)j * 128 + g * 32;
+      const uint8_t* p = bt[t] + j * lay.stage_stride;
       b.d[t][0] = ld16_stream(p);
-      b.d[t][1] = ld16_stream(p + 16);
+      b.d[t][1] = ld16_stream(p + lay.mfma_stride);
     }
     if constexpr (SCALES) b.s[t] = ld_u16(bst[t] + j * 8 + 2 * g);
   }
@@ -326,14 +348,20 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
   int col0;
   const uint8_t* bt[kNT];
   const uint8_t* bst[kNT];
+  BLayout lay{128, 16};  // routed E2M1 weights: checkpoint or MFMA-tiled layout (table pointer bit 0)
   if (GATEUP) {
     col0 = blockIdx.x * (kWaves * 32) + wave * 32;  // 32 intermediate columns: 2 gate + 2 up tiles
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int64_t row = col0 + 16 * t + r16;
-      bt[t] = ex.w1p + row * brow_bytes;
+      if (shared) {  // E4M3 rows, checkpoint layout (the E4M3 loads add their own offsets)
+        bt[t] = ex.w1p + row * brow_bytes;
+        bt[t + 2] = ex.w3p + row * brow_bytes;
+      } else {  // w1 and w3 of an expert share one layout
+        bt[t] = b_lane_base(ex.w1p, row, brow_bytes, NST, lane, lay);
+        bt[t + 2] = b_lane_base(ex.w3p, row, brow_bytes, NST, lane, lay);
+      }
       bst[t] = ex.w1s + row * bsrow;
-      bt[t + 2] = ex.w3p + row * brow_bytes;
       bst[t + 2] = ex.w3s + row * bsrow;
     }
   } else {
@@ -341,7 +369,7 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
 #pragma unroll
     for (int t = 0; t < kNT; ++t) {
       const int64_t row = col0 + 16 * t + r16;
-      bt[t] = ex.w2p + row * brow_bytes;
+      bt[t] = shared ? ex.w2p + row * brow_bytes : b_lane_base(ex.w2p, row, brow_bytes, NST, lane, lay);
       bst[t] = ex.w2s + row * bsrow;
     }
   }
@@ -372,13 +400,13 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < P && j < NST; ++j) {
       load_a<AFMT, false>(a[j % RING], abase, asbase, j, g);
-      load_b<false, B8>(b[j % RING], btp, bstp, j, g);
+      load_b<false, B8>(b[j % RING], btp, bstp, j, g, lay);
     }
 #pragma unroll
     for (int j = 0; j < NST; ++j) {
       if (j + P < NST) {
         load_a<AFMT, false>(a[(j + P) % RING], abase, asbase, j + P, g);
-        load_b<false, B8>(b[(j + P) % RING], btp, bstp, j + P, g);
+        load_b<false, B8>(b[(j + P) % RING], btp, bstp, j + P, g, lay);
       }
       if constexpr (P > 0) __builtin_amdgcn_sched_barrier(0);
       a[j % RING].s = stage_scales<NST>(as_row, j, r16, g);
@@ -499,14 +527,20 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
   int col0;
   const uint8_t* bt[kNT];
   const uint8_t* bst[kNT];
+  BLayout lay{128, 16};  // routed E2M1 weights: checkpoint or MFMA-tiled layout (table pointer bit 0)
   if (GATEUP) {
     col0 = blockIdx.x * (NW * 32) + wave * 32;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int64_t row = col0 + 16 * t + r16;
-      bt[t] = ex.w1p + row * brow_bytes;
+      if (shared) {  // E4M3 rows, checkpoint layout (the E4M3 loads add their own offsets)
+        bt[t] = ex.w1p + row * brow_bytes;
+        bt[t + 2] = ex.w3p + row * brow_bytes;
+      } else {  // w1 and w3 of an expert share one layout
+        bt[t] = b_lane_base(ex.w1p, row, brow_bytes, NST, lane, lay);
+        bt[t + 2] = b_lane_base(ex.w3p, row, brow_bytes, NST, lane, lay);
+      }
       bst[t] = ex.w1s + row * bsrow;
-      bt[t + 2] = ex.w3p + row * brow_bytes;
       bst[t + 2] = ex.w3s + row * bsrow;
     }
   } else {
@@ -514,7 +548,7 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
 #pragma unroll
     for (int t = 0; t < kNT; ++t) {
       const int64_t row = col0 + 16 * t + r16;
-      bt[t] = ex.w2p + row * brow_bytes;
+      bt[t] = shared ? ex.w2p + row * brow_bytes : b_lane_base(ex.w2p, row, brow_bytes, NST, lane, lay);
       bst[t] = ex.w2s + row * bsrow;
     }
   }
@@ -550,7 +584,7 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
     BStageT<B8> b[2];
 #pragma unroll
     for (int v = 0; v < LV; ++v) lreg[v] = ld16(lsrc[v]);
-    load_b<false, B8>(b[0], btp, bstp, 0, g);
+    load_b<false, B8>(b[0], btp, bstp, 0, g, lay);
 #pragma unroll
     for (int v = 0; v < LV; ++v) *(v4i*)&a_lds[0][ldst[v]] = lreg[v];
     __syncthreads();
@@ -559,7 +593,7 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
       if (j + 1 < NST) {
 #pragma unroll
         for (int v = 0; v < LV; ++v) lreg[v] = ld16(lsrc[v] + (j + 1) * ASB);
-        load_b<false, B8>(b[(j + 1) & 1], btp, bstp, j + 1, g);
+        load_b<false, B8>(b[(j + 1) & 1], btp, bstp, j + 1, g, lay);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll

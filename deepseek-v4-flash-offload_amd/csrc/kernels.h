@@ -16,6 +16,8 @@ struct Dsv4ExpertPtrs {
 
 hipError_t launch_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, uint16_t* out,
                                 int64_t n_elems, hipStream_t st);
+// packed E2M1 weights [N, K/2] <-> the MFMA-tiled layout (inverse = 1: tiled -> natural)
+hipError_t launch_mxfp4_tile(const uint8_t* src, uint8_t* dst, int64_t N, int64_t K, int inverse, hipStream_t st);
 // y[M, N] = bf16(x[M, K] @ dequant(packed, scales)^T), fp32 accumulation, M <= 16
 hipError_t launch_mxfp4_gemv(const uint16_t* x, int M, const uint8_t* packed, const uint8_t* scales, int N, int K,
                              uint16_t* y, hipStream_t st);

@@ -216,6 +216,44 @@ hipError_t launch_mxfp4_gemv(const uint16_t* x, int M, const uint8_t* packed, co
   return hipSuccess;
 }
 
+// ---------------------------------------------------------------------------
+// MFMA-tiled layout of packed E2M1 weights W [N, K/2] (N % 16 == 0, K % 256 == 0):
+//   tiled[nt][j][ji][g][r][e] = W[16 nt + r][128 j + 32 g + 16 ji + e]
+// (nt: 16-row tile, j: 256-wide K stage, ji: MFMA of the stage, lane L = r + 16 g,
+// e: byte of the lane's 16). Lane L of MFMA ji of stage j of a tile finds its
+// operand at ((nt * K/256 + j) * 2 + ji) * 1024 + 16 L, so every weight load of
+// the grouped GEMMs covers one contiguous 1 KB (eight whole 128-byte lines); in
+// the checkpoint layout each load instruction touches 16 rows x 64 bytes.
+// One thread moves one 16-byte chunk; `inverse` maps tiled back to natural.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mxfp4_tile_kernel(const u32x4* __restrict__ src, u32x4* __restrict__ dst,
+                                                         int64_t n_chunks, int64_t chunks_per_row, int nst,
+                                                         int inverse) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // natural chunk index
+  if (i >= n_chunks) return;
+  const int64_t n = i / chunks_per_row;
+  const int cb = (int)(i % chunks_per_row);
+  const int j = cb >> 3, c = cb & 7, g = c >> 1, ji = c & 1;
+  const int64_t nt = n >> 4;
+  const int r = (int)(n & 15);
+  const int64_t t = ((nt * nst + j) * 2 + ji) * 64 + (r + 16 * g);  // tiled chunk index
+  if (inverse)
+    dst[i] = src[t];
+  else
+    dst[t] = src[i];
+}
+
+hipError_t launch_mxfp4_tile(const uint8_t* src, uint8_t* dst, int64_t N, int64_t K, int inverse, hipStream_t st) {
+  const int64_t chunks_per_row = K / 32;  // 16 bytes = 32 E2M1 values
+  const int64_t n_chunks = N * chunks_per_row;
+  if (n_chunks == 0) return hipSuccess;
+  const int64_t grid = (n_chunks + 255) / 256;
+  if (grid > 0x7fffffffLL || K / 256 > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(mxfp4_tile_kernel, dim3((unsigned)grid), dim3(256), 0, st, (const u32x4*)src, (u32x4*)dst,
+                     n_chunks, chunks_per_row, (int)(K / 256), inverse);
+  return hipGetLastError();
+}
+
 hipError_t launch_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, uint16_t* out,
                                 int64_t n_elems, hipStream_t st) {
   const int64_t n_groups = n_elems / 8;

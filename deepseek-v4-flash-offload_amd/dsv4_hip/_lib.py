@@ -22,6 +22,7 @@ SCORING = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
 GEMM_BLOCK_M = 16
 MAX_EXPERTS = 512
 MAX_TOPK = 32
+TILED_WEIGHTS = 1  # pointer tag of an MFMA-tiled packed field in the expert table
 
 _c_p = ctypes.c_void_p
 _i32 = ctypes.c_int
@@ -34,6 +35,8 @@ SIGNATURES = {
     "dsv4_abi_version": (_i32, []),
     "dsv4_mxfp4_dequant_bf16": (_i32, [_c_p, _c_p, _c_p, _i64, _i64, _c_p]),
     "dsv4_mxfp4_gemv_bf16": (_i32, [_c_p, _i32, _c_p, _c_p, _i32, _i32, _c_p, _c_p]),
+    "dsv4_mxfp4_tile_weights": (_i32, [_c_p, _c_p, _i64, _i64, _i32, _c_p]),
+    "dsv4_mxfp4_tile_host": (_i32, [_c_p, _c_p, _i64, _i64]),
     "dsv4_fp8_act_quant": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "dsv4_mxfp4_act_quant": (_i32, [_c_p, _i64, _i64, _i32, _c_p, _c_p, _c_p, _c_p]),
     "dsv4_moe_route_workspace_bytes": (_i64, [_i32, _i32, _i32]),

@@ -293,11 +293,28 @@ def moe_combine(out_flat: torch.Tensor, topk_ids: torch.Tensor) -> torch.Tensor:
 _KEYS = ("w1p", "w1s", "w2p", "w2s", "w3p", "w3s")
 
 
-def expert_table(experts, n_experts: int, device) -> torch.Tensor:
+def tile_weights(w_packed: torch.Tensor, inverse: bool = False) -> torch.Tensor:
+    """Packed E2M1 weights [N, K/2] to the MFMA-tiled layout the grouped GEMMs
+    stream fastest (``dsv4_mxfp4_tile_weights``), or back with ``inverse``:
+    ``tiled[nt][j][ji][g][r][e] = w[16 nt + r][128 j + 32 g + 16 ji + e]``.
+    Returns a new uint8 tensor of the same shape; N % 16 == 0, K % 256 == 0."""
+    _dev(w_packed, "tile_weights")
+    w = _u8(w_packed.contiguous())
+    if w.dim() != 2:
+        raise ValueError("tile_weights: [N, K/2] packed weights required")
+    N, K = w.shape[0], w.shape[1] * 2
+    out = torch.empty_like(w)
+    call("dsv4_mxfp4_tile_weights", _p(w), _p(out), N, K, 1 if inverse else 0, _stream(w))
+    return out
+
+
+def expert_table(experts, n_experts: int, device, tiled: bool = False) -> torch.Tensor:
     """Device table [E, 6] (uint64 as int64) of the packed weight pointers.
 
     ``experts`` maps expert id -> dict with keys ``w{1,2,3}{p,s}`` (device
-    tensors, contiguous, any byte dtype). Missing experts get null entries."""
+    tensors, contiguous, any byte dtype). Missing experts get null entries.
+    ``tiled``: the packed fields hold the MFMA-tiled layout (``tile_weights``);
+    their pointers carry the table's layout tag (bit 0)."""
     tab = torch.zeros((n_experts, 6), dtype=torch.int64)
     items = experts.items() if hasattr(experts, "items") else enumerate(experts)
     for e, d in items:
@@ -310,7 +327,7 @@ def expert_table(experts, n_experts: int, device) -> torch.Tensor:
                 raise ValueError(f"expert {e} {k}: weights must be contiguous")
             if t.data_ptr() % 16:
                 raise ValueError(f"expert {e} {k}: weights must be 16-byte aligned")
-            tab[int(e), j] = t.data_ptr()
+            tab[int(e), j] = t.data_ptr() | (_lib.TILED_WEIGHTS if tiled and k.endswith("p") else 0)
     return tab.to(device)
 
 

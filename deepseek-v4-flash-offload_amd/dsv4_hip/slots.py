@@ -2,10 +2,15 @@
 
 A record is one expert's six packed tensors laid out back to back (256-byte
 aligned fields), identical in the pinned host pool and in every device slot,
-so a miss is a single host-to-device copy.
+so a miss is a single host-to-device copy. The three packed weight fields are
+stored in the MFMA-tiled layout the grouped GEMMs stream fastest (tiled once,
+on the host, when the expert is registered; env DSV4_TILED_WEIGHTS=0 keeps the
+checkpoint layout); the slot table tags them, and the views handed to callers
+(get_packed, the bf16 dequant path) are untiled back to the checkpoint layout.
 """
 
 import ctypes
+import os
 
 import numpy as np
 import torch
@@ -14,6 +19,14 @@ from . import _lib
 from ._lib import call
 
 FIELDS = ("w1p", "w1s", "w2p", "w2s", "w3p", "w3s")
+PACKED = ("w1p", "w2p", "w3p")
+
+
+def tile_host(a):
+    """Packed E2M1 bytes [N, K/2] in the MFMA-tiled layout (``dsv4_mxfp4_tile_weights``):
+    ``tiled[nt][j][ji][g][r][e] = a[16 nt + r][128 j + 32 g + 16 ji + e]``."""
+    N, KH = a.shape
+    return np.ascontiguousarray(a.reshape(N // 16, 16, KH // 128, 4, 2, 16).transpose(0, 2, 4, 3, 1, 5)).reshape(N, KH)
 
 
 def _align(n, a=256):
@@ -21,9 +34,11 @@ def _align(n, a=256):
 
 
 class SlotLayout:
-    """Field offsets/shapes/dtypes of one expert record."""
+    """Field offsets/shapes/dtypes of one expert record; ``tiled``: the packed
+    fields are stored MFMA-tiled (when every packed field has 16-row tiles and
+    256-wide K stages, and DSV4_TILED_WEIGHTS is not 0)."""
 
-    def __init__(self, tensors):
+    def __init__(self, tensors, tiled=None):
         self.shapes, self.dtypes, self.offsets, self.nbytes = {}, {}, {}, {}
         o = 0
         for k in FIELDS:
@@ -34,6 +49,11 @@ class SlotLayout:
             self.offsets[k] = o
             o = _align(o + self.nbytes[k])
         self.record_bytes = _align(o)
+        if tiled is None:
+            tiled = os.environ.get("DSV4_TILED_WEIGHTS", "1") != "0"
+        self.tiled = bool(tiled) and all(
+            len(self.shapes[k]) == 2 and self.shapes[k][0] % 16 == 0 and self.shapes[k][1] % 128 == 0
+            and self.nbytes[k] == self.shapes[k][0] * self.shapes[k][1] for k in PACKED)
 
     def matches(self, tensors):
         return all(tuple(tensors[k].shape) == self.shapes[k] and
@@ -80,7 +100,13 @@ class SlotCache:
             src = t.view(torch.uint8).numpy().reshape(-1) if t.element_size() == 1 else \
                 t.view(-1).view(torch.uint8).numpy()
             o = self.layout.offsets[k]
-            buf[o:o + src.size] = src
+            if self.layout.tiled and k in PACKED:  # tiled straight into the record
+                src = np.ascontiguousarray(src)
+                N, KH = self.layout.shapes[k]
+                call("dsv4_mxfp4_tile_host", src.ctypes.data_as(ctypes.c_void_p), ctypes.c_void_p(rec.value + o),
+                     N, 2 * KH)
+            else:
+                buf[o:o + src.size] = src
         self.keys_registered.add((int(layer), int(eid)))
         return bool(pinned.value)
 
@@ -110,30 +136,42 @@ class SlotCache:
     def release(self):
         call("dsv4_slots_release", self.h, self._stream())
 
+    def _natural(self, k, v):
+        """A field of a record as the caller registered it: tiled packed fields are
+        untiled into a new tensor, everything else is a view."""
+        if self.layout.tiled and k in PACKED:
+            from . import ops
+            v = ops.tile_weights(v.view(torch.uint8).view(self.layout.shapes[k]), inverse=True).view(-1)
+        return v.view(self.layout.dtypes[k]).view(self.layout.shapes[k])
+
     def slot_views(self, slot):
-        """Device tensors of one slot (views into the pool), in the registered shapes/dtypes."""
+        """Device tensors of one slot in the registered shapes/dtypes (views into the
+        pool; packed fields are checkpoint-layout copies when the pool is tiled)."""
         base = slot * self.layout.record_bytes
         out = {}
         for k in FIELDS:
             o = base + self.layout.offsets[k]
-            v = self.pool[o:o + self.layout.nbytes[k]]
-            out[k] = v.view(self.layout.dtypes[k]).view(self.layout.shapes[k])
+            out[k] = self._natural(k, self.pool[o:o + self.layout.nbytes[k]])
         return out
 
     def table(self, eids, slots, n_experts):
         """Device pointer table [E, 6] for the grouped GEMMs (pinned host staging, async copy)."""
         tab = torch.zeros((n_experts, len(FIELDS)), dtype=torch.int64, pin_memory=True)
-        tab.numpy()[np.asarray(eids, dtype=np.int64)] = self._slot_ptrs[np.asarray(slots, dtype=np.int64)]
+        ptrs = self._slot_ptrs[np.asarray(slots, dtype=np.int64)]
+        if self.layout.tiled:  # tag the packed fields as MFMA-tiled
+            ptrs = ptrs | np.array([_lib.TILED_WEIGHTS if k in PACKED else 0 for k in FIELDS], dtype=np.int64)
+        tab.numpy()[np.asarray(eids, dtype=np.int64)] = ptrs
         return tab.to(self.device, non_blocking=True)
 
     def copy_record(self, layer, eid, dst):
         call("dsv4_slots_copy_record", self.h, int(layer), int(eid), ctypes.c_void_p(dst.data_ptr()), self._stream())
 
     def record_views(self, buf):
+        """The fields of a record copied into ``buf``, as registered (see slot_views)."""
         out = {}
         for k in FIELDS:
             o = self.layout.offsets[k]
-            out[k] = buf[o:o + self.layout.nbytes[k]].view(self.layout.dtypes[k]).view(self.layout.shapes[k])
+            out[k] = self._natural(k, buf[o:o + self.layout.nbytes[k]])
         return out
 
     def lookup(self, layer, eid):

@@ -49,12 +49,16 @@ extern "C" {
 
 /* Per-expert weight pointers read by the grouped GEMMs (device array indexed
  * by expert id, 48 bytes per entry). Entries of experts that no token routes
- * to are never read. */
+ * to are never read. Packed fields are 16-byte aligned; a packed field whose
+ * pointer has bit 0 set (DSV4_TILED_WEIGHTS) is in the MFMA-tiled layout of
+ * dsv4_mxfp4_tile_weights instead of the checkpoint layout. The three packed
+ * fields of one expert share a layout. */
 typedef struct {
   const void* w1p; const void* w1s; /* gate  [I, D/2] + [I, D/32] */
   const void* w2p; const void* w2s; /* down  [D, I/2] + [D, I/32] */
   const void* w3p; const void* w3s; /* up    [I, D/2] + [I, D/32] */
 } dsv4_expert_ptrs;
+#define DSV4_TILED_WEIGHTS 1 /* OR into a packed-field pointer of dsv4_expert_ptrs */
 
 const char* dsv4_last_error(void);
 int dsv4_abi_version(void);
@@ -64,6 +68,18 @@ int dsv4_abi_version(void);
  * packed [n_rows, k/2], scales [n_rows, k/32], out [n_rows, k]; k % 32 == 0. */
 int dsv4_mxfp4_dequant_bf16(const void* packed, const void* scales, void* out, int64_t n_rows, int64_t k,
                             void* stream);
+
+/* Packed E2M1 weights [n_rows, k/2] (checkpoint layout, npu_ops.py:142-158) to the
+ * MFMA-tiled layout the grouped GEMMs stream fastest, or back (inverse = 1):
+ *   tiled[nt][j][ji][g][r][e] = packed[16 nt + r][128 j + 32 g + 16 ji + e]
+ * (16-row tiles nt, 256-wide K stages j, e < 16). A GEMM wave's weight load is
+ * then one contiguous 1 KB instead of 16 rows x 64 bytes. No counterpart in the
+ * reference (its weights stay in the checkpoint layout). n_rows % 16 == 0,
+ * k % 256 == 0; src and dst must not overlap. Scales keep their layout. */
+int dsv4_mxfp4_tile_weights(const void* src, void* dst, int64_t n_rows, int64_t k, int inverse, void* stream);
+/* The same tiling on the host (src, dst: host memory), for records written to a
+ * pinned pool before they are copied to the device. */
+int dsv4_mxfp4_tile_host(const void* src, void* dst, int64_t n_rows, int64_t k);
 
 /* y[m, n] = bf16(sum_k x[m, k] * dequant(packed, scales)[n, k]) with fp32
  * accumulation: the reference's CPU "dequant_fp4_weight + F.linear" check of a
