@@ -51,11 +51,19 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 #ifndef DSV4_GEMM_PREFETCH
 #define DSV4_GEMM_PREFETCH 1
 #endif
+// The 16-row kernel loads MFMA-tiled routed weights non-temporally: each weight
+// byte is read by one or a few row blocks, close together, and with one
+// contiguous 1 KB per wave load this measured 8% faster for the decode shape
+// than plain loads (on the checkpoint layout, 64 B from each of 16 rows per
+// load, non-temporal loads measured 9% slower, so that layout keeps plain
+// ones). The 64-row kernel keeps plain loads: its row blocks of one expert
+// re-read the weights from L2 (there non-temporal loads measured 2-4% slower).
 #ifndef DSV4_GEMM_NT_LOADS
-#define DSV4_GEMM_NT_LOADS 0
+#define DSV4_GEMM_NT_LOADS 1
 #endif
 
 constexpr int kBM = 16;
+constexpr bool kNtLoads = DSV4_GEMM_NT_LOADS != 0;
 constexpr int kNT = 4;        // 16-column output tiles per wave
 #ifndef DSV4_GEMM_WAVES
 #define DSV4_GEMM_WAVES 1
@@ -92,12 +100,12 @@ using BStage = BStageT<false>;
 typedef __attribute__((address_space(1))) const v4i gv4i;
 typedef __attribute__((address_space(1))) const uint16_t gu16;
 DSV4_DEV v4i ld16(const uint8_t* p) { return *(gv4i*)p; }
-#if DSV4_GEMM_NT_LOADS
-DSV4_DEV v4i ld16_stream(const uint8_t* p) { return __builtin_nontemporal_load((gv4i*)p); }
-#else
-// plain loads: measured faster than non-temporal ones for this pattern on MI355X
-DSV4_DEV v4i ld16_stream(const uint8_t* p) { return *(gv4i*)p; }
-#endif
+// Weight bytes: non-temporal when the kernel reads each of them about once.
+template <bool NT>
+DSV4_DEV v4i ld16_w(const uint8_t* p) {
+  if constexpr (NT) return __builtin_nontemporal_load((gv4i*)p);
+  else return *(gv4i*)p;
+}
 DSV4_DEV uint32_t ld_u16(const uint8_t* p) { return *(gu16*)p; }
 
 // ---------------------------------------------------------------------------
@@ -188,9 +196,11 @@ struct BLayout {
 DSV4_DEV bool tiled_ptr(const uint8_t* p) { return ((uintptr_t)p & 1u) != 0; }
 DSV4_DEV const uint8_t* untag(const uint8_t* p) { return (const uint8_t*)((uintptr_t)p & ~(uintptr_t)1); }
 // The lane's stage-0 chunk of weight row `row` (16-row tile row / 16) and the strides.
+// KNOWN_TILED: the caller has already found the tag set.
+template <bool KNOWN_TILED = false>
 DSV4_DEV const uint8_t* b_lane_base(const uint8_t* w, int64_t row, int64_t row_bytes, int nst, int lane,
                                     BLayout& lay) {
-  if (tiled_ptr(w)) {
+  if (KNOWN_TILED || tiled_ptr(w)) {
     lay = BLayout{2048, 1024};
     return untag(w) + (row >> 4) * (int64_t)nst * 2048 + 16 * lane;
   }
@@ -198,7 +208,7 @@ DSV4_DEV const uint8_t* b_lane_base(const uint8_t* w, int64_t row, int64_t row_b
   return w + row * row_bytes + 32 * (lane >> 4);
 }
 
-template <bool SCALES = true, bool B8 = false>
+template <bool SCALES = true, bool B8 = false, bool NT = false>
 DSV4_DEV void load_b(BStageT<B8>& b, const uint8_t* const* bt, const uint8_t* const* bst, int j, int g,
                      const BLayout& lay = BLayout{128, 16}) {
 #pragma unroll
@@ -207,14 +217,14 @@ DSV4_DEV void load_b(BStageT<B8>& b, const uint8_t* const* bt, const uint8_t* co
       const uint8_t* p = bt[t] + (int64_t)j * 256 + 16 * (g & 1) + 64 * (g >> 1);
 #pragma unroll
       for (int ji = 0; ji < 2; ++ji) {
-        const v4i lo = ld16_stream(p + 32 * ji);
-        const v4i hi = ld16_stream(p + 32 * ji + 128);
+        const v4i lo = ld16_w<NT>(p + 32 * ji);
+        const v4i hi = ld16_w<NT>(p + 32 * ji + 128);
         b.d[t][ji] = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
       }
     } else {
       const uint8_t* p = bt[t] + j * lay.stage_stride;
-      b.d[t][0] = ld16_stream(p);
-      b.d[t][1] = ld16_stream(p + lay.mfma_stride);
+      b.d[t][0] = ld16_w<NT>(p);
+      b.d[t][1] = ld16_w<NT>(p + lay.mfma_stride);
     }
     if constexpr (SCALES) b.s[t] = ld_u16(bst[t] + j * 8 + 2 * g);
   }
@@ -323,14 +333,10 @@ DSV4_DEV void quantise_h_mxfp4(const Dsv4GemmArgs& p, const uint32_t (*hb)[2], c
   }
 }
 
-// SH: the launch includes the shared expert's E4M3 blocks (a separate
-// instantiation, so the routed-only kernels keep their register budget).
-template <int AFMT, bool GATEUP, int NST, bool SH>
-__global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
+// NTW: the block's routed weights are MFMA-tiled and loaded non-temporally.
+template <int AFMT, bool GATEUP, int NST, bool SH, bool NTW>
+__attribute__((always_inline)) DSV4_DEV void moe_gemm_block(const Dsv4GemmArgs& p, const int mb, const int e) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int mb = blockIdx.y;
-  if (mb * kBM >= p.num_post_padded[0]) return;
-  const int e = p.block_expert[mb];
   // the shared expert's blocks carry id shared_expert and read its E4M3 weights
   const bool shared = SH && e == p.shared_expert;
   const Dsv4ExpertPtrs ex = shared ? p.shared : p.experts[e];
@@ -358,8 +364,8 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
         bt[t] = ex.w1p + row * brow_bytes;
         bt[t + 2] = ex.w3p + row * brow_bytes;
       } else {  // w1 and w3 of an expert share one layout
-        bt[t] = b_lane_base(ex.w1p, row, brow_bytes, NST, lane, lay);
-        bt[t + 2] = b_lane_base(ex.w3p, row, brow_bytes, NST, lane, lay);
+        bt[t] = b_lane_base<NTW>(ex.w1p, row, brow_bytes, NST, lane, lay);
+        bt[t + 2] = b_lane_base<NTW>(ex.w3p, row, brow_bytes, NST, lane, lay);
       }
       bst[t] = ex.w1s + row * bsrow;
       bst[t + 2] = ex.w3s + row * bsrow;
@@ -369,7 +375,7 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
 #pragma unroll
     for (int t = 0; t < kNT; ++t) {
       const int64_t row = col0 + 16 * t + r16;
-      bt[t] = shared ? ex.w2p + row * brow_bytes : b_lane_base(ex.w2p, row, brow_bytes, NST, lane, lay);
+      bt[t] = shared ? ex.w2p + row * brow_bytes : b_lane_base<NTW>(ex.w2p, row, brow_bytes, NST, lane, lay);
       bst[t] = ex.w2s + row * bsrow;
     }
   }
@@ -383,9 +389,12 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
   // MFMAs of stage j and a scheduling barrier keeps them there (a P+1 deep
   // register ring); with P = 0 the compiler schedules freely.
   // T0: first tile of this pass (E4M3 weights: two passes of kNT/2 tiles).
-  auto kloop = [&](auto b8, auto t0c) {
+  // NT: non-temporal weight loads (MFMA-tiled routed weights only: on the
+  // checkpoint layout they measured 9% slower than plain loads).
+  auto kloop = [&](auto b8, auto t0c, auto ntc) {
     constexpr bool B8 = decltype(b8)::value;
     constexpr int t0 = decltype(t0c)::value;
+    constexpr bool NT = decltype(ntc)::value;
     constexpr int NTB = BStageT<B8>::NTB;
     constexpr int P = DSV4_GEMM_PREFETCH;
     constexpr int RING = P + 1;
@@ -400,13 +409,13 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < P && j < NST; ++j) {
       load_a<AFMT, false>(a[j % RING], abase, asbase, j, g);
-      load_b<false, B8>(b[j % RING], btp, bstp, j, g, lay);
+      load_b<false, B8, NT>(b[j % RING], btp, bstp, j, g, lay);
     }
 #pragma unroll
     for (int j = 0; j < NST; ++j) {
       if (j + P < NST) {
         load_a<AFMT, false>(a[(j + P) % RING], abase, asbase, j + P, g);
-        load_b<false, B8>(b[(j + P) % RING], btp, bstp, j + P, g, lay);
+        load_b<false, B8, NT>(b[(j + P) % RING], btp, bstp, j + P, g, lay);
       }
       if constexpr (P > 0) __builtin_amdgcn_sched_barrier(0);
       a[j % RING].s = stage_scales<NST>(as_row, j, r16, g);
@@ -416,16 +425,21 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
       if constexpr (P > 0) __builtin_amdgcn_sched_barrier(0);
     }
   };
+  // The strides stay opaque to the optimiser: as constants (2048, 1024: past
+  // the loads' immediate-offset range) they led it to keep a 64-bit address
+  // per stage live, +20 VGPRs in the down GEMM.
+  if constexpr (NTW) asm volatile("" : "+s"(lay.stage_stride), "+s"(lay.mfma_stride));
+  auto routed = [&] { kloop(std::false_type{}, std::integral_constant<int, 0>{}, std::integral_constant<bool, NTW>{}); };
   if (have_w) {
     if constexpr (AFMT == 0 && SH) {  // E4M3 weights only meet E4M3 activations (bf16 profile)
       if (shared) {
-        kloop(std::true_type{}, std::integral_constant<int, 0>{});
-        kloop(std::true_type{}, std::integral_constant<int, kNT / 2>{});
+        kloop(std::true_type{}, std::integral_constant<int, 0>{}, std::false_type{});
+        kloop(std::true_type{}, std::integral_constant<int, kNT / 2>{}, std::false_type{});
       } else {
-        kloop(std::false_type{}, std::integral_constant<int, 0>{});
+        routed();
       }
     } else {
-      kloop(std::false_type{}, std::integral_constant<int, 0>{});
+      routed();
     }
   }
 
@@ -437,6 +451,23 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
   } else {
     store_tile<GATEUP, SH>(p, acc, mb * kBM, col0, g, r16);
   }
+}
+
+// SH: the launch includes the shared expert's E4M3 blocks (a separate
+// instantiation, so the routed-only kernels keep their register budget).
+// The weight layout is chosen per block, before anything else, so the two
+// bodies share no live values (a branch around the inner loop alone raised
+// the register count by up to 100 VGPRs).
+template <int AFMT, bool GATEUP, int NST, bool SH>
+__global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
+  const int mb = blockIdx.y;
+  if (mb * kBM >= p.num_post_padded[0]) return;
+  const int e = p.block_expert[mb];
+  const bool shared = SH && e == p.shared_expert;
+  if (kNtLoads && !shared && tiled_ptr(GATEUP ? p.experts[e].w1p : p.experts[e].w2p))
+    moe_gemm_block<AFMT, GATEUP, NST, SH, true>(p, mb, e);
+  else
+    moe_gemm_block<AFMT, GATEUP, NST, SH, false>(p, mb, e);
 }
 
 // ---------------------------------------------------------------------------
