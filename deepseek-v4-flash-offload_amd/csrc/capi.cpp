@@ -373,7 +373,9 @@ static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool sha
   w.status = take(sizeof(int32_t));
   w.xa = take(fp8 ? (int64_t)T * D : (int64_t)T * D / 2);
   w.xs = take((int64_t)T * D / 32);
-  w.h = take(2 * Rt * I);
+  // bf16 h only where the gate/up cannot quantise it in its epilogue (FP8
+  // blocks of 128 columns span four single-wave workgroups of the 16-row kernel)
+  w.h = (fp8 && bm == DSV4_GEMM_BLOCK_M) ? take(2 * Rt * I) : -1;
   w.ha = take(fp8 ? Rt * I : Rt * I / 2);
   w.hs = take(Rt * I / 32);
   w.out = take(2 * Rt * D);
@@ -500,7 +502,7 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
   gu.N = I;
   gu.topk_w = topk_w;
   gu.swiglu_limit = swiglu_limit;
-  gu.out = (uint16_t*)(base + w.h);
+  gu.out = hq_fused ? nullptr : (uint16_t*)(base + w.h);  // fused: h is never stored as bf16 (hq_skip_h)
   if (hq_fused) {
     gu.hq_mode = fp8 ? 1 : 2;
     gu.hq_rule = scale_rule;
