@@ -72,6 +72,12 @@ DSV4_DEV void route_topk_token(const RouteTopkArgs& a, int t, int lane) {
   int32_t* __restrict__ out_ids = a.out_ids;
   int32_t* status = a.status;
   const float ninf = -__builtin_inff();
+  // the bias and the token's input id are loaded with the partials (one memory
+  // latency, not two or three)
+  int64_t tok = tid2eid ? load_index(input_ids, ids_is64, t) : -1;
+  float bv[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) bv[j] = (bias && lane + 64 * j < E) ? bias[lane + 64 * j] : 0.f;
   float sc[EPL];
   // the S partials of each expert, summed in chunk order; up to 16 chunks' loads in flight
 #pragma unroll
@@ -114,19 +120,15 @@ DSV4_DEV void route_topk_token(const RouteTopkArgs& a, int t, int lane) {
     for (int j = 0; j < EPL; ++j) sc[j] = sqrtf(sc[j] > 20.f ? sc[j] : log1pf(expf(sc[j])));
   }
 
-  int64_t tok = -1;
-  if (tid2eid) {
-    tok = load_index(input_ids, ids_is64, t);
-    if (tok < 0 || tok >= vocab) {
-      if (status && lane == 0) atomicAdd(status, 1);
-      tok = -1;
-    }
+  if (tid2eid && (tok < 0 || tok >= vocab)) {
+    if (status && lane == 0) atomicAdd(status, 1);
+    tok = -1;
   }
   float choice[EPL];
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const int e = lane + 64 * j;
-    float c = sc[j] + (bias && e < E ? bias[e] : 0.f);
+    float c = sc[j] + bv[j];
     if (c != c) c = __builtin_inff();  // topk ranks NaN above every number
     choice[j] = (e < E) ? c : ninf;
   }
