@@ -103,6 +103,31 @@ def test_layer_on_tiled_weights_equals_checkpoint_layout(gpu, profile, T, K, E, 
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("profile", [PROFILE_BF16, PROFILE_A4W4])
+@pytest.mark.parametrize("T", [8, 300])
+def test_mixed_layouts_in_one_launch(gpu, profile, T):
+    # the 16-row kernel picks its weight loads per block from the table tag:
+    # tiled and checkpoint-layout experts side by side in one table
+    E, K, D, I = 32, 8, 1024, 512
+    ids = synth.zipf_topk(T, K, E, synth.rank_permutation(E, 5), np.random.default_rng(T + 9))
+    w = synth.routing_weights(T, K, 19)
+    x = synth.bf16_normal(np.random.default_rng(T + 2), (T, D)).to(gpu)
+    devw = {int(e): {k: torch.from_numpy(v).to(gpu) for k, v in synth.expert_weights(int(e), D, I).items()}
+            for e in np.unique(ids)}
+    tiled = _tiled_copy(devw)
+    runner = ops.LayerRunner(gpu, E, D, I)
+    ids_d, w_d = torch.from_numpy(ids).to(gpu), torch.from_numpy(w).to(gpu)
+    tab_nat = ops.expert_table(devw, E, gpu)
+    tab_til = ops.expert_table(tiled, E, gpu, tiled=True)
+    mixed = torch.where((torch.arange(E, device=gpu) % 2 == 0)[:, None], tab_til, tab_nat)
+    y_nat = runner.forward(x, ids_d, w_d, tab_nat, profile=profile, rule=RULE_OCP_FLOOR).clone()
+    y_mix = runner.forward(x, ids_d, w_d, mixed, profile=profile, rule=RULE_OCP_FLOOR)
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(y_mix), _bits(y_nat))
+    del devw, tiled
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("T", [8, 300])
 def test_tiled_routed_weights_with_the_shared_expert(gpu, T):
     E, K, D, I = 32, 8, 1024, 512
