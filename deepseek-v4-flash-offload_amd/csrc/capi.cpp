@@ -223,10 +223,10 @@ int64_t dsv4_moe_unpermute_workspace_bytes(int T, int Kmax) {
 }
 
 int dsv4_moe_unpermute(const void* out_sorted, const int32_t* row, int R, int T, int Kmax, int D, void* workspace,
-                       void* y, void* stream) {
+                       void* y, int32_t* status_out, void* stream) {
   REQUIRE(R >= 0 && T >= 0 && D >= 0, DSV4_ERR_SHAPE, "unpermute: negative size");
-  REQUIRE(Kmax > 0 && Kmax <= DSV4_MAX_TOPK, DSV4_ERR_UNSUPPORTED, "unpermute: Kmax=%d outside 1..%d", Kmax,
-          DSV4_MAX_TOPK);
+  REQUIRE(Kmax > 0 && Kmax <= DSV4_UNPERMUTE_MAX_ROWS, DSV4_ERR_UNSUPPORTED, "unpermute: Kmax=%d outside 1..%d",
+          Kmax, DSV4_UNPERMUTE_MAX_ROWS);
   REQUIRE(D % 8 == 0, DSV4_ERR_SHAPE, "unpermute: D=%d not a multiple of 8", D);
   if (T == 0 || D == 0) return DSV4_OK;
   REQUIRE(workspace && y && (R == 0 || (out_sorted && row)), DSV4_ERR_NULL, "unpermute: null pointer");
@@ -234,7 +234,8 @@ int dsv4_moe_unpermute(const void* out_sorted, const int32_t* row, int R, int T,
           "unpermute: misaligned buffer");
   int32_t* cnt = (int32_t*)workspace;
   int32_t* pos = cnt + T;
-  int32_t* status = pos + (int64_t)T * Kmax;
+  int32_t* status = status_out ? status_out : pos + (int64_t)T * Kmax;
+  REQUIRE(aligned(status, 4), DSV4_ERR_SHAPE, "unpermute: misaligned status");
   return hip_status(launch_moe_unpermute_rows((const uint16_t*)out_sorted, row, R, T, Kmax, D, cnt, pos, status,
                                               (uint16_t*)y, (hipStream_t)stream),
                     "unpermute launch");
@@ -293,7 +294,7 @@ static int check_gemm_common(int afmt, const void* a, const void* a_scale, const
           afmt);
   REQUIRE(R >= 0 && max_blocks >= 0, DSV4_ERR_SHAPE, "gemm: negative size");
   REQUIRE(moe_gemm_supported_kdim(Kdim), DSV4_ERR_UNSUPPORTED,
-          "gemm: reduction dim %d unsupported (512, 1024, 2048, 4096 or 8192)", Kdim);
+          "gemm: reduction dim %d unsupported (512, 1024, 2048 or 4096)", Kdim);
   REQUIRE(a && a_scale && sorted_ids && block_expert && npp && experts && out, DSV4_ERR_NULL,
           "gemm: null pointer");
   REQUIRE(aligned(a, 16) && aligned(a_scale, 4) && aligned(experts, 8), DSV4_ERR_SHAPE,

@@ -745,15 +745,16 @@ static hipError_t launch(const Dsv4GemmArgs& a, hipStream_t st) {
     case 4: launch_nst<GATEUP, 4>(a, st); break;
     case 8: launch_nst<GATEUP, 8>(a, st); break;
     case 16: launch_nst<GATEUP, 16>(a, st); break;
-    case 32: launch_nst<GATEUP, 32>(a, st); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
+// Reduction lengths 512..4096. Longer ones are not compiled: at K = 8192 the
+// fully unrolled K loops of the 64/128-row kernels spill to scratch.
 bool moe_gemm_supported_kdim(int kdim) {
   const int n = kdim / kStageK;
-  return kdim % kStageK == 0 && (n == 2 || n == 4 || n == 8 || n == 16 || n == 32);
+  return kdim % kStageK == 0 && (n == 2 || n == 4 || n == 8 || n == 16);
 }
 
 bool moe_gemm_supported_block_m(int bm) { return bm == 16 || bm == 64 || bm == 128; }

@@ -113,7 +113,7 @@ struct Dsv4GemmArgs {
 };
 hipError_t launch_moe_gemm_gateup(const Dsv4GemmArgs& a, hipStream_t st);
 hipError_t launch_moe_gemm_down(const Dsv4GemmArgs& a, hipStream_t st);
-bool moe_gemm_supported_kdim(int kdim);  // reduction lengths with a compiled kernel (512..8192, powers of two)
+bool moe_gemm_supported_kdim(int kdim);  // reduction lengths with a compiled kernel (512..4096, powers of two)
 bool moe_gemm_supported_block_m(int bm);  // 16 (decode kernel), 64 or 128 (tiled kernel)
 
 // Router top-k of one layer (per-token arguments of route_topk_token).

@@ -421,13 +421,18 @@ int dsv4_slots_sync(dsv4_slots* s) {
   return DSV4_OK;
 }
 
-int dsv4_slots_invalidate(dsv4_slots* s) {
+// Forgets every resident expert (offload.py:131-133 drops its cached dicts).
+// The slots of the last acquire may still be read by work the caller enqueued on
+// `compute_stream`: their release is recorded there first, so a later copy into
+// any of them waits for those readers (slot_rel_seq survives the clear).
+int dsv4_slots_invalidate(dsv4_slots* s, void* compute_stream) {
   SREQ(s, DSV4_ERR_NULL, "slots: null handle");
   std::lock_guard<std::mutex> g(s->mu);
   SHIP(hipSetDevice(s->device));
+  int rc = release_locked(s, (hipStream_t)compute_stream);
+  if (rc) return rc;
   SHIP(hipStreamSynchronize(s->copy_stream));
   s->lru.clear();
-  s->last_used.clear();
   std::fill(s->slot_copy_seq.begin(), s->slot_copy_seq.end(), 0);
   return DSV4_OK;
 }

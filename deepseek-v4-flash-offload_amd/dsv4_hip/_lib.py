@@ -22,6 +22,7 @@ SCORING = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}
 GEMM_BLOCK_M = 16
 MAX_EXPERTS = 512
 MAX_TOPK = 32
+UNPERMUTE_MAX_ROWS = 64  # rows one token may receive in moe_unpermute
 TILED_WEIGHTS = 1  # pointer tag of an MFMA-tiled packed field in the expert table
 
 _c_p = ctypes.c_void_p
@@ -49,7 +50,7 @@ SIGNATURES = {
                           + [_c_p, _i64, _c_p]),
     "dsv4_moe_permute": (_i32, [_c_p, _i64, _c_p, _i64, _i64, _c_p, _c_p]),
     "dsv4_moe_unpermute_workspace_bytes": (_i64, [_i32, _i32]),
-    "dsv4_moe_unpermute": (_i32, [_c_p, _c_p, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p]),
+    "dsv4_moe_unpermute": (_i32, [_c_p, _c_p, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p, _c_p]),
     "dsv4_moe_combine": (_i32, [_c_p, _c_p, _i32, _i32, _i32, _i32, _c_p, _c_p]),
     "dsv4_moe_gemm_gateup": (_i32, [_i32, _c_p, _c_p, _i32, _c_p, _c_p, _c_p, _i32, _i32, _i32, _c_p, _i32,
                                     _i32, _c_p, _f32, _c_p, _c_p]),
@@ -82,7 +83,7 @@ SIGNATURES = {
     "dsv4_slots_lookup": (_i32, [_c_p, _i32, _i32, ctypes.POINTER(_i32)]),
     "dsv4_slots_keys": (_i32, [_c_p, _c_p, _i32, ctypes.POINTER(_i32)]),
     "dsv4_slots_sync": (_i32, [_c_p]),
-    "dsv4_slots_invalidate": (_i32, [_c_p]),
+    "dsv4_slots_invalidate": (_i32, [_c_p, _c_p]),
     "dsv4_slots_stats": (_i32, [_c_p, _c_p]),
     "dsv4_slots_reset_stats": (_i32, [_c_p]),
 }

@@ -258,20 +258,37 @@ def moe_permute(x: torch.Tensor, row: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def moe_unpermute(out_sorted: torch.Tensor, row: torch.Tensor, T: int, kmax: Optional[int] = None):
-    """``zeros(T, D).index_add_(0, row, out.float()).bf16()`` (bit-exact)."""
+def moe_unpermute(out_sorted: torch.Tensor, row: torch.Tensor, T: int, kmax: Optional[int] = None,
+                  check: bool = True):
+    """``zeros(T, D).index_add_(0, row, out.float()).bf16()`` (bit-exact).
+
+    A token may receive up to ``kmax`` rows (default: R, capped at
+    ``UNPERMUTE_MAX_ROWS`` = 64). With ``check`` (default) the call reads back
+    the kernel's count of dropped rows (a host sync) and raises where
+    ``index_add_`` would not have dropped them: ``IndexError`` for a row whose
+    token is outside [0, T), ``ValueError`` for a token with more than ``kmax``
+    rows."""
     _dev(out_sorted, "moe_unpermute")
     if out_sorted.dtype != torch.bfloat16:
         raise TypeError("moe_unpermute: bf16 rows required")
     out_sorted = out_sorted.contiguous()
     row = row.to(torch.int32).contiguous()
     R, D = out_sorted.shape
+    if row.numel() != R:
+        raise ValueError(f"moe_unpermute: {row.numel()} row indices for {R} rows")
     if kmax is None:
-        kmax = max(1, -(-R // max(T, 1)))
+        kmax = max(1, min(R, _lib.UNPERMUTE_MAX_ROWS))
     ws = torch.empty(int(_lib.lib().dsv4_moe_unpermute_workspace_bytes(T, kmax)), dtype=torch.uint8,
                      device=out_sorted.device)
     y = torch.empty((T, D), dtype=torch.bfloat16, device=out_sorted.device)
-    call("dsv4_moe_unpermute", _p(out_sorted), _p(row), R, T, kmax, D, _p(ws), _p(y), _stream(out_sorted))
+    status = torch.zeros(1, dtype=torch.int32, device=out_sorted.device)
+    call("dsv4_moe_unpermute", _p(out_sorted), _p(row), R, T, kmax, D, _p(ws), _p(y), _p(status), _stream(out_sorted))
+    if check and T > 0 and R > 0:
+        dropped = int(status.item())
+        if dropped:
+            if bool(((row < 0) | (row >= T)).any()):
+                raise IndexError(f"moe_unpermute: row index outside [0, {T})")
+            raise ValueError(f"moe_unpermute: {dropped} row(s) beyond {kmax} rows per token were dropped")
     return y
 
 
@@ -331,18 +348,21 @@ def expert_table(experts, n_experts: int, device, tiled: bool = False) -> torch.
     return tab.to(device)
 
 
-def gemm_gateup(afmt, a, a_scale, a_row_div, al: AlignResult, table, D, I, topk_w_flat, swiglu_limit):
+def gemm_gateup(afmt, a, a_scale, a_row_div, al: AlignResult, table, D, I, topk_w_flat, swiglu_limit, out=None):
+    """h [R, I] bf16 by flat index (rows of ids the align skipped are left as they were in ``out``)."""
     R = al.T * al.K
-    h = torch.empty((R, I), dtype=torch.bfloat16, device=a.device)
+    h = out if out is not None else torch.empty((R, I), dtype=torch.bfloat16, device=a.device)
     call("dsv4_moe_gemm_gateup", afmt, _p(a), _p(a_scale), a_row_div, _p(al.sorted_ids), _p(al.block_expert),
          _p(al.num_post_padded), R, al.block_m, al.max_blocks, _p(table), D, I, _p(topk_w_flat),
          float(swiglu_limit or 0.0), _p(h), _stream(a))
     return h
 
 
-def gemm_down(afmt, a, a_scale, al: AlignResult, table, I, D):
+def gemm_down(afmt, a, a_scale, al: AlignResult, table, I, D, out=None):
+    """[R, D] bf16 by flat index (rows of ids the align skipped are left as they were in ``out``)."""
     R = al.T * al.K
-    out = torch.empty((R, D), dtype=torch.bfloat16, device=a.device)
+    if out is None:
+        out = torch.empty((R, D), dtype=torch.bfloat16, device=a.device)
     call("dsv4_moe_gemm_down", afmt, _p(a), _p(a_scale), _p(al.sorted_ids), _p(al.block_expert),
          _p(al.num_post_padded), R, al.block_m, al.max_blocks, _p(table), I, D, _p(out), _stream(a))
     return out

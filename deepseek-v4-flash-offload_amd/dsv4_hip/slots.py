@@ -154,6 +154,16 @@ class SlotCache:
             out[k] = self._natural(k, self.pool[o:o + self.layout.nbytes[k]])
         return out
 
+    def slot_copy(self, slot):
+        """Like ``slot_views``, but every field is a new tensor that later acquires
+        cannot overwrite (the copies are enqueued on the current stream, before
+        any later copy into the slot can start)."""
+        out = self.slot_views(slot)
+        for k in FIELDS:
+            if not (self.layout.tiled and k in PACKED):  # untiled fields are new tensors already
+                out[k] = out[k].clone()
+        return out
+
     def table(self, eids, slots, n_experts):
         """Device pointer table [E, 6] for the grouped GEMMs (pinned host staging, async copy)."""
         tab = torch.zeros((n_experts, len(FIELDS)), dtype=torch.int64, pin_memory=True)
@@ -189,7 +199,9 @@ class SlotCache:
         call("dsv4_slots_sync", self.h)
 
     def invalidate(self):
-        call("dsv4_slots_invalidate", self.h)
+        """Forget every resident expert; reads already enqueued on the current
+        stream finish before any slot is overwritten."""
+        call("dsv4_slots_invalidate", self.h, self._stream())
 
     def stats(self):
         s = np.zeros(9, dtype=np.int64)

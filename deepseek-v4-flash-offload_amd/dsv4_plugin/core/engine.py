@@ -76,7 +76,9 @@ class ExpertOffloadEngine:
             return False
         layer, w, kind = parsed
         self._shared.setdefault(layer, {})[w + ("s" if kind == "scale" else "")] = tensor.detach().to("cpu")
-        self._shared_dev.pop(layer, None)
+        # a re-captured tensor (weight reload) invalidates the layer's prepared copy on every device
+        for key in [k for k in self._shared_dev if k[0] == layer]:
+            del self._shared_dev[key]
         return True
 
     def get_shared(self, layer: int, device):

@@ -27,7 +27,6 @@ import weakref
 
 import numpy as np
 import torch
-import torch.nn.functional as F
 from torch import nn
 
 from dsv4_plugin.core.engine import get_engine, is_expert_weight
@@ -167,36 +166,18 @@ class OffloadDeepseekV4MoE(_BASE):
     # -- routing ---------------------------------------------------------------
     def _route(self, hs: torch.Tensor, input_ids):
         """``noaux_tc`` + score function routing: biased scores choose, unbiased
-        scores weigh, renormalise, scale (``deepseek_v4.py:118-148``).
-
-        Device tensors go through the HIP router (``dsv4_moe_route``: ids int32,
-        each token's picks in descending biased score). Host tensors use the
-        same math in torch, as the reference writes it."""
+        scores weigh, renormalise, scale (``deepseek_v4.py:118-148``), on the HIP
+        router (``dsv4_moe_route``: ids int32, each token's picks in descending
+        biased score). There is no host implementation: CPU tensors raise."""
         if self.hash and input_ids is None:
             raise RuntimeError("hash-layer routing needs input_ids (forward_context.input_ids is missing)")
-        if hs.is_cuda:
-            return _ops.route(hs, self.gate.weight, self.topk, self.scoring_func,
-                              bias=None if self.hash else self.gate.e_score_correction_bias,
-                              renormalize=bool(self.renormalize), scale=float(self.routed_scaling_factor),
-                              tid2eid=self.gate.tid2eid if self.hash else None, input_ids=input_ids)
-        gating = F.linear(hs.float(), self.gate.weight)
-        if self.scoring_func == "softmax":
-            scores = gating.softmax(dim=-1)
-        elif self.scoring_func == "sigmoid":
-            scores = gating.sigmoid()
-        else:  # sqrtsoftplus
-            scores = F.softplus(gating).sqrt()
-        if self.hash:
-            indices = self.gate.tid2eid[input_ids.to(torch.long).flatten()]
-        else:
-            bias = self.gate.e_score_correction_bias
-            choice = scores if bias is None else scores + bias.to(scores.dtype)
-            indices = torch.topk(choice, k=self.topk, dim=-1, sorted=False)[1]
-        weights = scores.gather(1, indices.to(torch.long))
-        if self.renormalize:
-            weights = weights / weights.sum(dim=-1, keepdim=True)
-        weights = weights * self.routed_scaling_factor
-        return weights, indices
+        if not hs.is_cuda:
+            raise RuntimeError(f"_route: the HIP router needs ROCm device tensors (got {hs.device}); "
+                               "there is no CPU implementation")
+        return _ops.route(hs, self.gate.weight, self.topk, self.scoring_func,
+                          bias=None if self.hash else self.gate.e_score_correction_bias,
+                          renormalize=bool(self.renormalize), scale=float(self.routed_scaling_factor),
+                          tid2eid=self.gate.tid2eid if self.hash else None, input_ids=input_ids)
 
     # -- experts ---------------------------------------------------------------
     def _expert_table(self, indices: torch.Tensor, device):
@@ -234,6 +215,13 @@ class OffloadDeepseekV4MoE(_BASE):
         x = hs if (hs.dtype == torch.bfloat16 and hs.is_contiguous()) else hs.to(torch.bfloat16).contiguous()
         if T == 0:
             return torch.zeros_like(hs)
+        cap = getattr(getattr(self.engine, "bank", None), "packed_capacity", None)
+        if cap is not None and hasattr(self.engine, "acquire_table"):
+            ids_h = indices.detach().to("cpu").numpy().reshape(-1)
+            uniq = np.unique(ids_h[(ids_h >= 0) & (ids_h < self.n_routed_experts)])
+            if uniq.size > max(int(cap), 1):
+                return self._run_experts_in_parts(x, weights, indices, profile, uniq, max(int(cap), 1),
+                                                  shared).type_as(hs)
         table, inter = self._expert_table(indices, hs.device)
         if _PREFETCH_NEXT:
             self._prefetch_next(hs, input_ids)
@@ -241,6 +229,55 @@ class OffloadDeepseekV4MoE(_BASE):
         y = _runner(hs.device, self.n_routed_experts, D, inter).forward(
             x, indices, weights, table, profile=profile, rule=_RULES[_MX_RULE], swiglu_limit=limit, shared=shared)
         return y.type_as(hs)
+
+    def _run_experts_in_parts(self, x, weights, indices, profile, uniq, cap, shared):
+        """The routed layer when it routes to more experts than the packed slot cache
+        holds (the reference's per-expert ``get_packed`` works at any capacity by
+        evicting). The experts are acquired ``cap`` at a time; each part runs the
+        grouped GEMMs on the routed rows of its experts (the other ids are masked
+        out of its layout) into one buffer of per-row outputs, and a single combine
+        sums every token's rows in ascending expert id, so the result equals the
+        one-part layer bit for bit. With a fused shared expert, its output (the
+        layer with no routed rows) is added as forward adds the shared MLP's."""
+        T, D = x.shape
+        K = indices.shape[1]
+        E = self.n_routed_experts
+        ids = indices.to(torch.int32).contiguous()
+        w = weights.to(torch.float32).contiguous().reshape(-1)
+        rule = _RULES[_MX_RULE]
+        limit = self.swiglu_limit if (self.swiglu_limit and self.swiglu_limit > 0) else 0.0
+        fp8 = profile == _lib.PROFILE_BF16
+        if fp8:
+            q = _ops.fp8_act_quant(x, 128, want_codes=True, want_e8m0x4=True)
+            xa, xs, afmt = q["codes"], q["e8m0x4"], _lib.AFMT_E4M3
+        else:
+            xa, xs, _ = _ops.mxfp4_act_quant(x, rule)
+            afmt = _lib.AFMT_E2M1
+        out = None
+        h = None
+        for i in range(0, uniq.size, cap):
+            part = uniq[i:i + cap]
+            table, _ = self.engine.acquire_table(self.layer_idx, part, E)
+            inter = self.engine.bank._layout.shapes["w1p"][0]
+            if out is None:
+                out = torch.empty((T * K, D), dtype=torch.bfloat16, device=x.device)
+                h = torch.empty((T * K, inter), dtype=torch.bfloat16, device=x.device)
+            keep = torch.isin(ids, torch.from_numpy(part.astype(np.int32)).to(x.device))
+            al = _ops.moe_align(torch.where(keep, ids, torch.full_like(ids, -1)), None, E)
+            _ops.gemm_gateup(afmt, xa, xs, K, al, table, D, inter, w, limit, out=h)
+            if fp8:
+                q = _ops.fp8_act_quant(h, 128, want_codes=True, want_e8m0x4=True)
+                ha, has = q["codes"], q["e8m0x4"]
+            else:
+                ha, has, _ = _ops.mxfp4_act_quant(h, rule)
+            _ops.gemm_down(afmt, ha, has, al, table, inter, D, out=out)
+        y = _ops.moe_combine(out, ids)
+        if shared is not None:
+            none = torch.full_like(ids, -1)
+            ys = _runner(x.device, E, D, h.shape[1]).forward(x, none, weights, table, profile=profile, rule=rule,
+                                                               swiglu_limit=limit, shared=shared)
+            y = (y.float() + ys.float()).to(torch.bfloat16)
+        return y
 
     def _routed(self, hs: torch.Tensor, input_ids=None, shared=None) -> torch.Tensor:
         """Routed-expert output ``[T, D]`` (``deepseek_v4.py:150-197``); the a4w4

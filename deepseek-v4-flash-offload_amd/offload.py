@@ -10,10 +10,9 @@ Same constructor, methods and ``stats()`` keys as the reference
 * ``get`` keeps the reference's bf16 LRU of dequantised experts
   (``capacity`` entries); a miss copies the packed record to the device and
   dequantises it with the HIP kernel (bit-exact with ``dequant_fp4_weight``);
-* ``get_packed`` serves device views of the expert's slot in the native LRU
-  slot cache (``packed_capacity`` slots, default 4 x ``capacity`` as in the
-  reference). The views stay valid for work enqueued on the current stream
-  before the next ``get_packed``/``acquire_table`` call that may evict it;
+* ``get_packed`` makes the expert resident in the native LRU slot cache
+  (``packed_capacity`` slots, default 4 x ``capacity`` as in the reference)
+  and returns device copies of its six tensors, which the caller owns;
 * ``acquire_table`` is the batched fast path used by the MoE layer: one call
   per (layer, step) makes all routed experts resident and returns the device
   pointer table of the grouped GEMMs. Misses are copied on a side stream and
@@ -136,10 +135,12 @@ class ExpertBank:
 
     # -- device packed slot cache -------------------------------------------
     def get_packed(self, layer, eid):
-        """Packed device views ``{"w{1,2,3}p": [N, K/2], "w{1,2,3}s": [N, K/32]}``."""
+        """Packed device tensors ``{"w{1,2,3}p": [N, K/2], "w{1,2,3}s": [N, K/32]}``,
+        owned by the caller like the reference's (``offload.py:122-124``): copies
+        of the slot, so a later acquire that reuses the slot cannot change them."""
         self._need_gpu("get_packed")
         slots, _ = self._slots.acquire(int(layer), [int(eid)])
-        return self._slots.slot_views(int(slots[0]))
+        return self._slots.slot_copy(int(slots[0]))
 
     def acquire_table(self, layer, expert_ids, n_experts):
         """Make every expert in ``expert_ids`` resident; returns (device pointer table [E, 6], n_miss)."""

@@ -165,11 +165,15 @@ int dsv4_moe_permute(const void* src, int64_t n_src, const int32_t* row, int64_t
 
 /* y = bf16(zeros(T, D) fp32 .index_add_(0, row, out_sorted.float())), summed in
  * ascending sorted position per token, bit-exact. Replaces
- * deepseek_v4.py:195-197 / 243-245. Each token may appear at most Kmax times.
+ * deepseek_v4.py:195-197 / 243-245. Kmax (1..DSV4_UNPERMUTE_MAX_ROWS) bounds the
+ * rows any one token may receive; a row beyond that bound, or whose token is
+ * outside [0, T), is dropped and counted in `status` (device int32 [1],
+ * overwritten; nullable), where index_add_ would have summed it or raised.
  * workspace: dsv4_moe_unpermute_workspace_bytes(T, Kmax) bytes of device memory. */
+#define DSV4_UNPERMUTE_MAX_ROWS 64
 int64_t dsv4_moe_unpermute_workspace_bytes(int T, int Kmax);
 int dsv4_moe_unpermute(const void* out_sorted, const int32_t* row, int R, int T, int Kmax, int D, void* workspace,
-                       void* y, void* stream);
+                       void* y, int32_t* status, void* stream);
 
 /* Same combine for rows stored by flat index (row t*K+k = the k-th pick of
  * token t): each token's rows are summed in ascending expert id, which is the
@@ -186,7 +190,7 @@ int dsv4_moe_combine(const void* out_flat, const void* topk_ids, int ids_int64, 
  * [rows, D/2] (E2M1), a_scale [rows, D/32]. h_out: bf16 [R, I] by flat index.
  * block_m (the moe_align block size) is 16 (single-wave workgroups, decode),
  * 64 or 128 (LDS-tiled workgroups: each weight fragment serves 4 or 8 row
- * tiles); D and I must be 256 * 2^n (512..8192) and I a multiple of 128. */
+ * tiles); D and I must be 256 * 2^n (512..4096) and I a multiple of 128. */
 int dsv4_moe_gemm_gateup(int afmt, const void* a, const void* a_scale, int a_row_div, const int32_t* sorted_ids,
                          const int32_t* block_expert, const int32_t* num_post_padded, int R, int block_m,
                          int max_blocks, const void* expert_table, int D, int I, const float* topk_w,
@@ -309,7 +313,10 @@ int dsv4_slots_copy_record(dsv4_slots* s, int layer, int eid, void* dst, void* s
 int dsv4_slots_lookup(dsv4_slots* s, int layer, int eid, int32_t* slot);
 int dsv4_slots_keys(dsv4_slots* s, int64_t* out, int max, int* n);
 int dsv4_slots_sync(dsv4_slots* s);
-int dsv4_slots_invalidate(dsv4_slots* s);
+/* Drops every resident expert (ExpertBank.invalidate, offload.py:131-133). The
+ * slots of the last acquire are released on `compute_stream` first, so copies
+ * into them made after this call wait for the reads already enqueued there. */
+int dsv4_slots_invalidate(dsv4_slots* s, void* compute_stream);
 /* stats[9] = hits, misses, evictions, prefetched, bytes_h2d, copies, cached, capacity, pinned */
 int dsv4_slots_stats(dsv4_slots* s, int64_t* stats);
 int dsv4_slots_reset_stats(dsv4_slots* s);

@@ -131,8 +131,9 @@ def routed_bf16(x_bf16, topk_ids, topk_w, experts, n_experts=256, swiglu_limit=1
 
 
 def routed_a4w4(x_bf16, topk_ids, topk_w, experts, n_experts=256, swiglu_limit=10.0,
-                rule="ocp_floor"):
-    """a4w4 profile of ``_routed_mxfp4`` (``deepseek_v4.py:199-245``)."""
+                rule="ocp_floor", workers=1):
+    """a4w4 profile of ``_routed_mxfp4`` (``deepseek_v4.py:199-245``). ``workers``
+    as in ``routed_bf16``."""
     x_bf16 = np.asarray(x_bf16, np.uint16)
     T, D = x_bf16.shape
     al = moe_align(topk_ids, topk_w, n_experts)
@@ -142,23 +143,29 @@ def routed_a4w4(x_bf16, topk_ids, topk_w, experts, n_experts=256, swiglu_limit=1
     I = experts[int(al["active"][0])]["w1p"].shape[0] if R else 0
     gate = np.zeros((R, I), np.float32)
     up = np.zeros((R, I), np.float32)
-    o = 0
+    starts = np.concatenate([[0], np.cumsum(al["group_list"])]).astype(np.int64)
+    groups = [(int(e), int(starts[i]), int(starts[i + 1])) for i, e in enumerate(al["active"])]
     W = {}
-    for e, c in zip(al["active"], al["group_list"]):
-        W[int(e)] = _expert_f32(experts, e)
-        w1, w3, _ = W[int(e)]
-        gate[o:o + c] = Q.f32_to_bf16_f32(matmul_nt(xa[o:o + c], w1))       # :231
-        up[o:o + c] = Q.f32_to_bf16_f32(matmul_nt(xa[o:o + c], w3))         # :232
-        o += c
+
+    def gate_up(g):
+        e, a, b = g
+        W[e] = _expert_f32(experts, e)
+        w1, w3, _ = W[e]
+        gate[a:b] = Q.f32_to_bf16_f32(matmul_nt(xa[a:b], w1))           # :231
+        up[a:b] = Q.f32_to_bf16_f32(matmul_nt(xa[a:b], w3))             # :232
+
+    _map(gate_up, groups, workers)
     h = swiglu(gate, up, al["s_w"], swiglu_limit)                        # :234-237
     h_bf16 = Q.f32_to_bf16_bits(h)
     _, hp, hs = Q.dynamic_mx_quant(h_bf16, rule)                         # :240
     ha = Q.fp4_codes_to_f32(hp, hs)
     out = np.zeros((R, D), np.float32)
-    o = 0
-    for e, c in zip(al["active"], al["group_list"]):
-        out[o:o + c] = matmul_nt(ha[o:o + c], W[int(e)][2])             # :241
-        o += c
+
+    def down(g):
+        e, a, b = g
+        out[a:b] = matmul_nt(ha[a:b], W[e][2])                           # :241
+
+    _map(down, groups, workers)
     out_bf16 = Q.f32_to_bf16_bits(out)
     y = unpermute(out_bf16, al["row"], T)                                # :243-245
     return {"align": al, "xp": xp, "xs": xs, "gate": gate, "up": up, "h": h,

@@ -82,6 +82,16 @@ def test_gemm_and_layer_validation():
     rc, msg = _err(lib.dsv4_moe_gemm_gateup(0, None, None, 8, None, None, None, 64, 16, 10, None, 4000, 2048,
                                             None, ctypes.c_float(10.0), None, None))
     assert rc == -3 and "512" in msg
+    # K = 8192 is not compiled (its unrolled K loops spill): rejected before any launch
+    for kd in (8192, 256):
+        rc, msg = _err(lib.dsv4_moe_gemm_gateup(0, None, None, 8, None, None, None, 64, 16, 10, None, kd, 2048,
+                                                None, ctypes.c_float(10.0), None, None))
+        assert rc == -3 and "unsupported" in msg, kd
+    rc, msg = _err(lib.dsv4_moe_gemm_down(0, None, None, None, None, None, 64, 16, 10, None, 8192, 4096, None, None))
+    assert rc == -3 and "unsupported" in msg
+    # unpermute: at most 64 rows per token (one wave ranks them)
+    rc, msg = _err(lib.dsv4_moe_unpermute(None, None, 8, 2, 65, 64, None, None, None, None))
+    assert rc == -3 and "Kmax" in msg
     n = ctypes.c_int64(0)
     assert lib.dsv4_moe_layer_workspace_bytes(8, 8, 256, 4096, 2048, 0, ctypes.byref(n)) == 0
     assert n.value > 2 * 64 * 4096  # holds at least the [R, D] bf16 expert outputs

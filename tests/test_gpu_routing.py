@@ -108,3 +108,35 @@ def test_unpermute_and_combine_bitexact(gpu, T, K, D):
                          torch.from_numpy(ids).to(gpu))
     torch.cuda.synchronize()
     assert np.array_equal(yf.cpu().view(torch.int16).numpy().view(np.uint16), want)
+
+
+@pytest.mark.parametrize("R,T,seed", [(3, 2, 0), (200, 10, 1), (64, 1, 2), (513, 40, 3)])
+def test_unpermute_uneven_rows_per_token(gpu, R, T, seed):
+    # index_add_ semantics for any row -> token map (not only K rows per token): uneven
+    # counts, a token with no rows, all rows on one token (64 = the per-token bound)
+    rng = np.random.default_rng(seed)
+    row = np.zeros(R, np.int32) if R == 3 or T == 1 else rng.integers(0, T, R).astype(np.int32)
+    if T > 2:
+        row[row == T - 1] = 0          # token T-1 receives nothing
+    D = 512
+    out = Q.f32_to_bf16_bits((rng.standard_normal((R, D)) * 3).astype(np.float32))
+    ref = torch.zeros(T, D).index_add_(0, torch.from_numpy(row.astype(np.int64)),
+                                       torch.from_numpy(Q.bf16_bits_to_f32(out))).to(torch.bfloat16)
+    want = ref.view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(RT.unpermute(out, row, T), want)
+    y = ops.moe_unpermute(torch.from_numpy(out.view(np.int16)).view(torch.bfloat16).to(gpu),
+                          torch.from_numpy(row).to(gpu), T)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), want)
+
+
+def test_unpermute_rejects_what_it_would_drop(gpu):
+    D = 64
+    out = torch.zeros(70, D, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError, match="beyond 64 rows"):
+        ops.moe_unpermute(out, torch.zeros(70, dtype=torch.int32, device=gpu), 2)   # 70 rows on one token
+    bad = torch.tensor([0, 1, 2, 5], dtype=torch.int32, device=gpu)
+    with pytest.raises(IndexError):
+        ops.moe_unpermute(out[:4], bad, 3)
+    with pytest.raises(IndexError):
+        ops.moe_unpermute(out[:4], torch.tensor([0, -1, 1, 1], dtype=torch.int32, device=gpu), 3)

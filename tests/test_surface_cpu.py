@@ -147,18 +147,9 @@ def test_moe_module_constructs_without_vllm(monkeypatch):
     assert h.hash and h.gate.tid2eid.shape == (100, 4)
     with pytest.raises(RuntimeError, match="input_ids"):
         h._route(torch.zeros(2, 512), None)
-    # routing math runs in torch (device-agnostic) and matches model_npu.Gate semantics
-    torch.manual_seed(0)
-    m.gate.weight.data.normal_()
-    m.gate.e_score_correction_bias.data.normal_()
-    x = torch.randn(3, 512)
-    w, idx = m._route(x, None)
-    scores = torch.nn.functional.softplus(x.float() @ m.gate.weight.T).sqrt()
-    ref_idx = (scores + m.gate.e_score_correction_bias).topk(4, dim=-1)[1]
-    assert torch.equal(idx.sort(-1).values, ref_idx.sort(-1).values)
-    ref_w = scores.gather(1, idx)
-    ref_w = ref_w / ref_w.sum(-1, keepdim=True) * 1.5
-    assert torch.allclose(w, ref_w)
+    # routing runs on the HIP router only: host tensors raise instead of taking a CPU path
+    with pytest.raises(RuntimeError, match="no CPU implementation"):
+        m._route(torch.randn(3, 512), None)
 
 
 def test_tee_keeps_a_copy_of_the_shared_expert():
@@ -190,6 +181,20 @@ def test_tee_keeps_a_copy_of_the_shared_expert():
     assert sorted(engine._shared) == [1, 2] and sorted(engine._shared[1]) == ["w1", "w1s", "w2", "w2s", "w3", "w3s"]
     assert int(engine._shared[2]["w3s"][0, 0]) == names.index("model.layers.2.ffn.shared_experts.w3.scale")
     assert engine.get_shared(5, "cpu") is None      # nothing captured for layer 5
+
+
+def test_recaptured_shared_tensor_drops_every_prepared_copy_of_its_layer():
+    # get_shared caches per (layer, device); a re-captured tensor of layer 1 must drop
+    # layer 1's prepared copies on every device and leave other layers' alone
+    engine = ExpertOffloadEngine(slot_capacity=4, device="cpu")
+    for l in (1, 2):
+        for w in ("w1", "w2", "w3"):
+            for k in ("weight", "scale"):
+                engine.capture_shared(f"layers.{l}.ffn.shared_experts.{w}.{k}", torch.zeros(2, 2, dtype=torch.uint8))
+    engine._shared_dev = {(1, "cuda:0"): "old", (1, "cuda:1"): "old", (2, "cuda:0"): "kept"}
+    assert engine.capture_shared("layers.1.ffn.shared_experts.w2.weight", torch.ones(2, 2, dtype=torch.uint8))
+    assert engine._shared_dev == {(2, "cuda:0"): "kept"}
+    assert int(engine._shared[1]["w2"][0, 0]) == 1
 
 
 def test_resident_table_needs_a_device_bank():
