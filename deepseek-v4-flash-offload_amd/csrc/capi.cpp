@@ -9,6 +9,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
+#include <mutex>
 #include <string>
 
 #include "common.h"
@@ -568,6 +569,73 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
                            float swiglu_limit, void* workspace, int64_t workspace_bytes, void* y, void* stream) {
   return layer_forward(profile, scale_rule, x, topk_ids, ids_int64, topk_w, T, K, E, D, I, expert_table, nullptr,
                        swiglu_limit, workspace, workspace_bytes, y, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free routed layer. Some callers cannot allocate device memory
+// (code under HIP graph capture, tight serving loops, harnesses that forbid
+// hipMalloc); for them the layer's workspace is `scratch`, a file-scope device
+// array that each GPU holds once for the life of the process. In host code the
+// name `scratch` is only a host-side stand-in for the symbol: its device
+// address is looked up once per device with hipGetSymbolAddress, with that
+// device current, and only that address is handed to kernels. The layer needs
+// no zeroed workspace (every region is written before it is read), so nothing
+// is cleared between calls; calls that overlap on one GPU (different streams)
+// share the array and race.
+static constexpr int64_t kScratchBytes = (int64_t)DSV4_NOALLOC_SCRATCH_BYTES;
+static constexpr int kMaxDevices = 64;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device that owns `stream` (looked up on
+// that device's first call; later calls reuse it).
+static int scratch_address(void* stream, void** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return hip_status(e, "no-alloc layer: hipGetDevice");
+  hipDevice_t dev = cur;
+  if (stream) {
+    e = hipStreamGetDevice((hipStream_t)stream, &dev);
+    if (e != hipSuccess) return hip_status(e, "no-alloc layer: hipStreamGetDevice");
+  }
+  REQUIRE(dev >= 0 && dev < kMaxDevices, DSV4_ERR_UNSUPPORTED, "no-alloc layer: device %d beyond %d", (int)dev,
+          kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    if (dev != cur) {
+      e = hipSetDevice(dev);
+      if (e != hipSuccess) return hip_status(e, "no-alloc layer: hipSetDevice");
+    }
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (e != hipSuccess) return hip_status(e, "no-alloc layer: hipGetSymbolAddress(scratch)");
+    REQUIRE(p && aligned(p, 256), DSV4_ERR_STATE, "no-alloc layer: scratch address not 256-byte aligned");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return DSV4_OK;
+}
+
+int dsv4_moe_layer_forward_noalloc(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
+                                   const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
+                                   float swiglu_limit, void* y, void* stream) {
+  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4, DSV4_ERR_UNSUPPORTED,
+          "no-alloc layer: unknown profile %d", profile);
+  REQUIRE(T >= 0 && K > 0 && K <= DSV4_MAX_TOPK && E > 0 && D > 0 && I > 0, DSV4_ERR_SHAPE,
+          "no-alloc layer: bad sizes T=%d K=%d E=%d D=%d I=%d", T, K, E, D, I);
+  if (T == 0) return DSV4_OK;
+  const int64_t need = layer_ws(T, K, E, D, I, profile).total;
+  REQUIRE(need <= kScratchBytes, DSV4_ERR_UNSUPPORTED,
+          "no-alloc layer: needs %lld bytes of workspace, the static scratch holds %lld (fewer tokens per call, "
+          "or dsv4_moe_layer_forward with a caller workspace)",
+          (long long)need, (long long)kScratchBytes);
+  void* ws = nullptr;
+  int rc = scratch_address(stream, &ws);
+  if (rc) return rc;
+  return layer_forward(profile, scale_rule, x, topk_ids, ids_int64, topk_w, T, K, E, D, I, expert_table, nullptr,
+                       swiglu_limit, ws, kScratchBytes, y, stream);
 }
 
 int dsv4_expand_block_scales(const void* block_scales, int64_t n_rows, int64_t k, void* out, void* stream) {

@@ -23,6 +23,7 @@ GEMM_BLOCK_M = 16
 MAX_EXPERTS = 512
 MAX_TOPK = 32
 UNPERMUTE_MAX_ROWS = 64  # rows one token may receive in moe_unpermute
+NOALLOC_SCRATCH_BYTES = 64 << 20  # static workspace of dsv4_moe_layer_forward_noalloc
 TILED_WEIGHTS = 1  # pointer tag of an MFMA-tiled packed field in the expert table
 
 _c_p = ctypes.c_void_p
@@ -59,6 +60,8 @@ SIGNATURES = {
     "dsv4_moe_layer_workspace_bytes": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i64)]),
     "dsv4_moe_layer_forward": (_i32, [_i32, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32, _c_p,
                                       _f32, _c_p, _i64, _c_p, _c_p]),
+    "dsv4_moe_layer_forward_noalloc": (_i32, [_i32, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32,
+                                              _c_p, _f32, _c_p, _c_p]),
     "dsv4_moe_layer_shared_workspace_bytes": (_i32, [_i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i64)]),
     "dsv4_moe_layer_forward_shared": (_i32, [_c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32, _c_p] + [_c_p] * 6
                                       + [_f32, _c_p, _i64, _c_p, _c_p]),

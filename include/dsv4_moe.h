@@ -222,6 +222,21 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
                            const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
                            float swiglu_limit, void* workspace, int64_t workspace_bytes, void* y, void* stream);
 
+/* dsv4_moe_layer_forward without a workspace argument and without allocating:
+ * no counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc). The workspace is a static device array of
+ * DSV4_NOALLOC_SCRATCH_BYTES (64 MiB) that each GPU the library runs on holds
+ * until the process ends; a call whose dsv4_moe_layer_workspace_bytes exceeds
+ * it returns DSV4_ERR_UNSUPPORTED (about 500 tokens at top-8, hidden 4096,
+ * inter 2048). The array is per device and shared by every call on it: calls
+ * that overlap on one GPU (on different streams) race. Outputs equal
+ * dsv4_moe_layer_forward's bit for bit. */
+#define DSV4_NOALLOC_SCRATCH_BYTES (64 << 20)
+int dsv4_moe_layer_forward_noalloc(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
+                                   const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
+                                   float swiglu_limit, void* y, void* stream);
+
 /* The same layer with the shared expert folded in as one more group of the
  * grouped GEMMs (bf16 profile): OffloadDeepseekV4MoE.forward's
  * `out = self._routed(hs) + self.shared_experts(hs)` (deepseek_v4.py:262-264)
