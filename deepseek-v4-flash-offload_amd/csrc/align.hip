@@ -60,21 +60,29 @@ __device__ int block_exclusive_scan(int v, int* lds_waves, int* out_total) {
 // the padding sentinel is R + n_shared.
 // write = false: only off_u/off_p (for workgroups that recompute the layout
 // to scatter their own entries).
+// hot (optional, chunked align only): experts with at least hot->hot_min rows get
+// their own layout of kHotBlockM-row blocks (hot->sorted_ids / block_expert /
+// num_post_padded) and no blocks in the main layout; off_p then holds -1 - (their
+// padded offset in the hot layout), which tells the scatter where an entry goes.
 template <int NT>
 __device__ void align_layout(int c, int bad, int R, int E, int block_m, int max_blocks, int n_shared,
-                             const Dsv4AlignOut& o, int* off_u, int* off_p, bool write = true) {
+                             const Dsv4AlignOut& o, int* off_u, int* off_p, bool write = true,
+                             const Dsv4AlignHot* hot = nullptr) {
   constexpr int kWaves = NT / 64;
   __shared__ int scan_tmp[kWaves];
-  __shared__ int totals[3];
+  __shared__ int totals[4];
   const int tid = threadIdx.x;
-  const int padded = ((c + block_m - 1) / block_m) * block_m;
+  const bool is_hot = hot && hot->hot_min > 0 && c >= hot->hot_min;
+  const int padded = is_hot ? 0 : ((c + block_m - 1) / block_m) * block_m;
+  const int padded_h = is_hot ? ((c + kHotBlockM - 1) / kHotBlockM) * kHotBlockM : 0;
   const int shared_padded = ((n_shared + block_m - 1) / block_m) * block_m;
   const int ou = block_exclusive_scan<NT>(c, scan_tmp, &totals[0]);
   const int op = block_exclusive_scan<NT>(padded, scan_tmp, &totals[1]) + shared_padded;
   const int oa = block_exclusive_scan<NT>(c > 0 ? 1 : 0, scan_tmp, &totals[2]);
+  const int oph = hot ? block_exclusive_scan<NT>(padded_h, scan_tmp, &totals[3]) : 0;
   if (tid < E) {
     off_u[tid] = ou;
-    off_p[tid] = op;
+    off_p[tid] = is_hot ? -1 - oph : op;
   }
   if (!write) {
     __syncthreads();
@@ -82,7 +90,7 @@ __device__ void align_layout(int c, int bad, int R, int E, int block_m, int max_
   }
   if (tid < E) {
     if (o.counts) o.counts[tid] = c;
-    if (o.expert_start) o.expert_start[tid] = op;
+    if (o.expert_start) o.expert_start[tid] = is_hot ? -1 : op;
     if (o.active) o.active[tid] = -1;
   }
   __syncthreads();
@@ -96,6 +104,17 @@ __device__ void align_layout(int c, int bad, int R, int E, int block_m, int max_
     for (int b = b0; b < b1; ++b) o.block_expert[b] = tid;
     const int p1 = min(op + padded, cap);
     for (int p = op + c; p < p1; ++p) o.sorted_ids[p] = pad_id;
+    if (is_hot) {
+      const int cap_h = hot->max_blocks * kHotBlockM;
+      const int h0 = oph / kHotBlockM, h1 = min((oph + padded_h) / kHotBlockM, hot->max_blocks);
+      for (int b = h0; b < h1; ++b) hot->block_expert[b] = tid;
+      const int q1 = min(oph + padded_h, cap_h);
+      for (int q = oph + c; q < q1; ++q) hot->sorted_ids[q] = pad_id;
+    }
+  }
+  if (hot && tid == 0) {
+    const int total_h = totals[3];
+    hot->num_post_padded[0] = min(total_h, hot->max_blocks * kHotBlockM);
   }
   // the shared expert's group: rows R + i in order, ahead of the routed experts
   for (int i = tid; i < shared_padded; i += NT) {
@@ -107,7 +126,8 @@ __device__ void align_layout(int c, int bad, int R, int E, int block_m, int max_
   if (tid == 0) {
     o.num_post_padded[0] = min(total_padded, cap);
     if (o.num_active) o.num_active[0] = totals[2];
-    if (o.status) o.status[0] = bad + (total_blocks > max_blocks ? (1 << 30) : 0);
+    const bool hot_over = hot && totals[3] > hot->max_blocks * kHotBlockM;
+    if (o.status) o.status[0] = bad + ((total_blocks > max_blocks || hot_over) ? (1 << 30) : 0);
   }
   __syncthreads();
 }
@@ -122,7 +142,7 @@ template <typename IdT, int NT>
 __device__ void align_scatter_range(const IdT* __restrict__ ids, const float* __restrict__ topk_w, int i0, int i1,
                                     int K, int E, int block_m, int max_blocks, const int* off_u, const int* off_p,
                                     int* running, int* wcount, const Dsv4AlignOut& o, bool have_id0,
-                                    long long id0) {
+                                    long long id0, const Dsv4AlignHot* hot = nullptr) {
   constexpr int kWaves = NT / 64;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int nbits = 0;
@@ -148,13 +168,20 @@ __device__ void align_scatter_range(const IdT* __restrict__ ids, const float* __
       int r = running[e] + rank;
       for (int w = 0; w < wave; ++w) r += wcount[w * (E + 1) + e];
       const int u = off_u[e] + r;
-      const int p = off_p[e] + r;
+      const int op = off_p[e];
       if (o.order) o.order[u] = i;
       if (o.s_e) o.s_e[u] = e;
       if (o.s_w) o.s_w[u] = topk_w ? topk_w[i] : 0.0f;
       if (o.row) o.row[u] = i / K;
-      if (p < max_blocks * block_m) o.sorted_ids[p] = i;
-      if (o.padded_pos) o.padded_pos[i] = p;
+      if (op >= 0) {
+        const int p = op + r;
+        if (p < max_blocks * block_m) o.sorted_ids[p] = i;
+        if (o.padded_pos) o.padded_pos[i] = p;
+      } else {  // hot layout (only when hot is given: off_p >= 0 otherwise)
+        const int q = -1 - op + r;
+        if (q < hot->max_blocks * kHotBlockM) hot->sorted_ids[q] = i;
+        if (o.padded_pos) o.padded_pos[i] = -1 - q;
+      }
     }
     __syncthreads();
     for (int ex = tid; ex < E + 1; ex += NT) {
@@ -245,7 +272,9 @@ template <typename IdT, int NT>
 __global__ __launch_bounds__(NT) void align_scatter_kernel(const IdT* __restrict__ ids,
                                                            const float* __restrict__ topk_w, int R, int K, int E,
                                                            int C, int block_m, int max_blocks, int n_shared,
-                                                           const int* __restrict__ cc, Dsv4AlignOut o) {
+                                                           const int* __restrict__ cc, Dsv4AlignOut o,
+                                                           Dsv4AlignHot hot) {
+  const Dsv4AlignHot* hp = hot.hot_min > 0 ? &hot : nullptr;
   constexpr int kWaves = NT / 64;
   extern __shared__ int lds[];
   int* off_u = lds;                  // [E]
@@ -273,9 +302,9 @@ __global__ __launch_bounds__(NT) void align_scatter_kernel(const IdT* __restrict
   }
   for (int i = tid; i < kWaves * (E + 1); i += NT) wcount[i] = 0;
   __syncthreads();
-  align_layout<NT>(tid < E ? tot : 0, bad, R, E, block_m, max_blocks, n_shared, o, off_u, off_p, c == 0);
+  align_layout<NT>(tid < E ? tot : 0, bad, R, E, block_m, max_blocks, n_shared, o, off_u, off_p, c == 0, hp);
   align_scatter_range<IdT, NT>(ids, topk_w, c * kAlignChunk, min(R, (c + 1) * kAlignChunk), K, E, block_m,
-                               max_blocks, off_u, off_p, running, wcount, o, false, 0);
+                               max_blocks, off_u, off_p, running, wcount, o, false, 0, hp);
 }
 
 template <typename IdT, int NT>
@@ -394,7 +423,8 @@ int64_t align_chunked_scratch_bytes(int R, int E) {
 hipError_t launch_moe_align_chunked(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K, int E,
                                     int block_m, int max_blocks, const Dsv4AlignOut& o, const uint16_t* x,
                                     int64_t n_elems, int qfmt, int rule, void* q_codes, void* q_scale,
-                                    hipStream_t st, int n_shared, void* scratch) {
+                                    hipStream_t st, int n_shared, void* scratch, const Dsv4AlignHot* hot) {
+  const Dsv4AlignHot hv = hot ? *hot : Dsv4AlignHot{};
   const int C = (R + kAlignChunk - 1) / kAlignChunk;
   int* cc = (int*)scratch;
   const int64_t n_groups = x ? n_elems / 8 : 0;
@@ -419,7 +449,7 @@ hipError_t launch_moe_align_chunked(const void* topk_ids, int ids_int64, const f
 #define DSV4_SC(IDT, NT)                                                                                       \
   hipLaunchKernelGGL((align_scatter_kernel<IDT, NT>), dim3(C), dim3(NT),                                      \
                      sizeof(int) * (size_t)(E + E + (E + 1) + (NT / 64) * (E + 1)), st, (const IDT*)topk_ids, \
-                     topk_w, R, K, E, C, block_m, max_blocks, n_shared, cc, o)
+                     topk_w, R, K, E, C, block_m, max_blocks, n_shared, cc, o, hv)
   if (E <= 256) {
     if (ids_int64) DSV4_SC(long long, 256); else DSV4_SC(int32_t, 256);
   } else {

@@ -9,6 +9,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
+#include <stdlib.h>
+#include <algorithm>
 #include <mutex>
 #include <string>
 
@@ -308,7 +310,7 @@ int dsv4_moe_gemm_gateup(int afmt, const void* a, const void* a_scale, int a_row
                          int max_blocks, const void* expert_table, int D, int I, const float* topk_w,
                          float swiglu_limit, void* h_out, void* stream) {
   REQUIRE(moe_gemm_supported_block_m(block_m), DSV4_ERR_UNSUPPORTED,
-          "gemm: block_m %d unsupported (16, 64 or 128)", block_m);
+          "gemm: block_m %d unsupported (16, 64, 128 or 256)", block_m);
   REQUIRE(I > 0 && I % 128 == 0, DSV4_ERR_UNSUPPORTED, "gemm gate/up: I=%d not a multiple of 128", I);
   REQUIRE(a_row_div > 0, DSV4_ERR_SHAPE, "gemm gate/up: a_row_div=%d", a_row_div);
   if (R == 0 || max_blocks == 0) return DSV4_OK;
@@ -316,6 +318,8 @@ int dsv4_moe_gemm_gateup(int afmt, const void* a, const void* a_scale, int a_row
                              expert_table, D, h_out);
   if (rc) return rc;
   REQUIRE(topk_w, DSV4_ERR_NULL, "gemm gate/up: null routing weights");
+  REQUIRE(block_m != 256 || moe_gemm_big_supported(D, I, true), DSV4_ERR_UNSUPPORTED,
+          "gemm gate/up: 256-row blocks need D a multiple of 1024 and I of 128 (D=%d, I=%d)", D, I);
   Dsv4GemmArgs g{afmt, (const uint8_t*)a, afmt == DSV4_AFMT_E4M3 ? (int64_t)D : (int64_t)D / 2,
                  (const uint8_t*)a_scale, a_row_div, sorted_ids, block_expert, num_post_padded, R, block_m,
                  max_blocks, (const Dsv4ExpertPtrs*)expert_table, D, I, topk_w, swiglu_limit,
@@ -327,12 +331,14 @@ int dsv4_moe_gemm_down(int afmt, const void* a, const void* a_scale, const int32
                        const int32_t* block_expert, const int32_t* num_post_padded, int R, int block_m,
                        int max_blocks, const void* expert_table, int I, int D, void* out, void* stream) {
   REQUIRE(moe_gemm_supported_block_m(block_m), DSV4_ERR_UNSUPPORTED,
-          "gemm: block_m %d unsupported (16, 64 or 128)", block_m);
+          "gemm: block_m %d unsupported (16, 64, 128 or 256)", block_m);
   REQUIRE(D > 0 && D % 256 == 0, DSV4_ERR_UNSUPPORTED, "gemm down: D=%d not a multiple of 256", D);
   if (R == 0 || max_blocks == 0) return DSV4_OK;
   int rc = check_gemm_common(afmt, a, a_scale, sorted_ids, block_expert, num_post_padded, R, max_blocks,
                              expert_table, I, out);
   if (rc) return rc;
+  REQUIRE(block_m != 256 || (moe_gemm_big_supported(I, D, false) && aligned(out, 16)), DSV4_ERR_UNSUPPORTED,
+          "gemm down: 256-row blocks need I a multiple of 1024, D of 256 and a 16-byte aligned output");
   Dsv4GemmArgs g{afmt, (const uint8_t*)a, afmt == DSV4_AFMT_E4M3 ? (int64_t)I : (int64_t)I / 2,
                  (const uint8_t*)a_scale, 1, sorted_ids, block_expert, num_post_padded, R, block_m, max_blocks,
                  (const Dsv4ExpertPtrs*)expert_table, I, D, nullptr, 0.0f, (uint16_t*)out};
@@ -351,7 +357,21 @@ struct LayerWs {
   int64_t sorted_ids, block_expert, npp, status, xa, xs, h, ha, hs, out, align_scratch, route_part, total;
   int max_blocks;
   int bm;
+  // hot layout (experts with at least hot_min rows, 256-row blocks, large-tile kernel); hot_min 0: none
+  int hot_min, max_blocks_h;
+  int64_t sorted_ids_h, block_expert_h, npp_h;
 };
+
+// Experts with at least this many routed rows run in 256-row blocks on the
+// large-tile kernel once the chunked align is in use (above 2048 routed rows);
+// the rest keep 64-row blocks. DSV4_HOT_ROWS overrides it (0: never), read once.
+static int hot_rows_threshold() {
+  static const int v = [] {
+    const char* s = getenv("DSV4_HOT_ROWS");
+    return s ? atoi(s) : 256;
+  }();
+  return v;
+}
 
 // Rows per M block: 16 (decode kernel, ~1-4 rows per active expert) below 2048
 // routed rows, 64 (tiled kernel, weight tiles reused across 4 row subtiles)
@@ -383,6 +403,15 @@ static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool sha
   w.out = take(2 * Rt * D);
   w.align_scratch = R > kAlignSmallRows ? take(align_chunked_scratch_bytes((int)R, E)) : 0;
   w.route_part = routed ? take(dsv4_moe_route_workspace_bytes(T, D, E)) : -1;  // router partial logits
+  const int hot = hot_rows_threshold();
+  if (R > kAlignSmallRows && hot > 0 && moe_gemm_big_supported(D, I, true) && moe_gemm_big_supported(I, D, false)) {
+    w.hot_min = hot;
+    // each hot expert holds >= hot_min rows: blocks <= R/256 + min(E, R/hot_min) + 1
+    w.max_blocks_h = (int)(R / kHotBlockM + std::min<int64_t>(E, R / hot) + 1);
+    w.sorted_ids_h = take(sizeof(int32_t) * (int64_t)w.max_blocks_h * kHotBlockM);
+    w.block_expert_h = take(sizeof(int32_t) * (int64_t)w.max_blocks_h);
+    w.npp_h = take(sizeof(int32_t));
+  }
   w.total = o;
   return w;
 }
@@ -474,11 +503,16 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
     }
     if (rc) return rc;
   }
+  Dsv4AlignHot hot{};
+  if (w.hot_min > 0)
+    hot = Dsv4AlignHot{w.hot_min, w.max_blocks_h, (int32_t*)(base + w.sorted_ids_h), (int32_t*)(base + w.block_expert_h),
+                       (int32_t*)(base + w.npp_h)};
   if (!aligned_already) rc = hip_status(
       R > kAlignSmallRows
           ? launch_moe_align_chunked(topk_ids, ids_int64, nullptr, R, K, E, bm, w.max_blocks, ao, (const uint16_t*)x,
                                      (int64_t)T * D, fp8 ? 0 : 1, scale_rule, base + w.xa, base + w.xs,
-                                     (hipStream_t)stream, n_sh, base + w.align_scratch)
+                                     (hipStream_t)stream, n_sh, base + w.align_scratch,
+                                     w.hot_min > 0 ? &hot : nullptr)
           : launch_moe_align_quant(topk_ids, ids_int64, nullptr, R, K, E, bm, w.max_blocks, ao, (const uint16_t*)x,
                                    (int64_t)T * D, fp8 ? 0 : 1, scale_rule, base + w.xa, base + w.xs,
                                    (hipStream_t)stream, n_sh),
@@ -520,6 +554,20 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
   }
   rc = hip_status(launch_moe_gemm_gateup(gu, (hipStream_t)stream), "gemm gate/up launch");
   if (rc) return rc;
+  // the hot layout's 256-row blocks (routed rows only) on the large-tile kernel
+  auto hot_args = [&](Dsv4GemmArgs g) {
+    g.sorted_ids = hot.sorted_ids;
+    g.block_expert = hot.block_expert;
+    g.num_post_padded = hot.num_post_padded;
+    g.block_m = kHotBlockM;
+    g.max_blocks = hot.max_blocks;
+    g.has_shared = 0;
+    return g;
+  };
+  if (w.hot_min > 0) {
+    rc = hip_status(launch_moe_gemm_gateup(hot_args(gu), (hipStream_t)stream), "gemm gate/up (large tiles) launch");
+    if (rc) return rc;
+  }
   if (!hq_fused) {  // FP8 blocks of 128 columns span four single-wave workgroups
     rc = dsv4_fp8_act_quant(base + w.h, Rt, I, 128, nullptr, base + w.ha, nullptr, base + w.hs, stream);
     if (rc) return rc;
@@ -547,6 +595,10 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
   }
   rc = hip_status(launch_moe_gemm_down(dn, (hipStream_t)stream), "gemm down launch");
   if (rc) return rc;
+  if (w.hot_min > 0) {
+    rc = hip_status(launch_moe_gemm_down(hot_args(dn), (hipStream_t)stream), "gemm down (large tiles) launch");
+    if (rc) return rc;
+  }
   // ids outside [0, E) were skipped by the align (never computed) and add nothing here
   REQUIRE(aligned(y, 16), DSV4_ERR_SHAPE, "layer: y not 16-byte aligned");
   const uint16_t* outp = (const uint16_t*)(base + w.out);

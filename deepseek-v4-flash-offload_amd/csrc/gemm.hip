@@ -739,6 +739,7 @@ static void launch_nst(const Dsv4GemmArgs& a, hipStream_t st) {
 
 template <bool GATEUP>
 static hipError_t launch(const Dsv4GemmArgs& a, hipStream_t st) {
+  if (a.block_m == kHotBlockM && !a.has_shared) return launch_moe_gemm_big(a, GATEUP, st);  // gemm_big.hip
   if (a.block_m != 16 && a.block_m != 64 && a.block_m != 128) return hipErrorInvalidValue;
   switch (a.Kdim / kStageK) {
     case 2: launch_nst<GATEUP, 2>(a, st); break;
@@ -757,7 +758,7 @@ bool moe_gemm_supported_kdim(int kdim) {
   return kdim % kStageK == 0 && (n == 2 || n == 4 || n == 8 || n == 16);
 }
 
-bool moe_gemm_supported_block_m(int bm) { return bm == 16 || bm == 64 || bm == 128; }
+bool moe_gemm_supported_block_m(int bm) { return bm == 16 || bm == 64 || bm == 128 || bm == kHotBlockM; }
 
 hipError_t launch_moe_gemm_gateup(const Dsv4GemmArgs& a, hipStream_t st) { return launch<true>(a, st); }
 

@@ -1,0 +1,563 @@
+// Large-tile grouped GEMM for experts that receive many rows (prefill).
+//
+// moe_align gives every expert with at least `hot_min` routed rows its own
+// layout of 256-row M blocks (the "hot" layout); this kernel runs those
+// blocks. One workgroup = 4 waves = 256 rows x 256 weight rows (gate/up: 128
+// gate + the 128 matching up rows; down: 256 output rows of W2). Both operand
+// tiles of each 64-k stage go through LDS - the A rows gathered through
+// sorted_ids, the weight rows from the expert's slot - so every weight byte a
+// block brings from L2 serves 256 rows (the 16/64-row kernels re-read an
+// expert's weights once per 16 or 64 rows) and every A byte 256 weight rows.
+// Each wave (one per SIMD) owns 128 rows x 128 weight rows: 4 x 4 tiles of
+// v_mfma_scale_f32_32x32x64_f8f6f4 whose 256 accumulator registers live in
+// the AGPRs, so every fragment read from LDS feeds four MFMAs. The 32x32x64
+// form carries twice the FLOPs per operand byte of the 16x16x128 one (and ran
+// fp4 x fp4 at 7.25 PFLOP/s against 6.7 in an MFMA-loop probe on this part).
+//
+// Operands move global -> LDS with global_load_lds_dwordx4 (lane i of one
+// instruction writes its 16 bytes at the instruction's LDS base + 16 i): no
+// staging registers, so a ring of NB stage slots keeps NB - 1 stages of loads
+// in flight (96 KB per CU with FP8 A). With one workgroup per CU there are no
+// other waves to hide the load latency behind; the depth of the ring does.
+// Each 1-KB chunk is laid out in the order the MFMA lanes read it, with an XOR
+// swizzle that puts the 16 lanes of each ds_read_b128 pass on distinct banks.
+//
+// Operand layouts of the 32x32x64 scaled MFMA (measured on gfx950):
+//   E2M1 A/B: lane (r = l%32, g = l/32) holds k [32g, 32g+32) of row r in 16
+//             bytes, low nibble first.
+//   E4M3 A  : lane (r, g) holds k [16g, 16g+16) in bytes 0-15 and
+//             [32+16g, 32+16g+16) in bytes 16-31.
+//   scales  : lane (r, g) supplies the E8M0 of 32-block g of its row/column.
+//   C       : register i of lane l holds C[8(i/4) + 4(l/32) + i%4][l%32].
+// Chunks of one stage (slot i = bytes [16 i, 16 i + 16) of a chunk):
+//   E4M3 A chunk c : rows 16c + r (r < 16), 64 bytes each; slot 4r + (p ^ (r/4 % 4))
+//                    holds bytes [16p, 16p + 16) of row r's stage.
+//   E2M1 A chunk c : rows 32c + r (r < 32), 32 bytes each; slot 2r + (p ^ (r/8 % 2))
+//                    holds bytes [16p, 16p + 16).
+//   weight chunk c : weight rows 32c + 16h + r (h < 2, r < 16); slot 32h + 16j + r
+//                    holds bytes [16j, 16j + 16) of the row's stage (in an
+//                    MFMA-tiled slot, two whole 256-byte runs of each 16-row tile).
+#include "common.h"
+#include "kernels.h"
+#include "quant_dev.h"
+
+namespace {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(1))) const v4i gv4i;
+typedef __attribute__((address_space(1))) const void gvoid;
+typedef __attribute__((address_space(3))) void lvoid;
+
+constexpr int kBM = 256;     // rows per block
+constexpr int kBN = 256;     // weight rows per block
+constexpr int kNT = 256;     // threads (4 waves, one per SIMD)
+constexpr int kKS = 64;      // k per stage
+constexpr int kSS = 16;      // stages per scale super-stage (1024 k)
+constexpr int kSPitch = 40;  // scale row pitch: the 32 rows of a byte read land on distinct banks
+
+template <int AFMT>
+struct Big {
+  static constexpr int ACH = AFMT == 0 ? 16 : 8;     // 1-KB A chunks per stage
+  static constexpr int BCH = kBN * (kKS / 2) / 1024;  // 1-KB weight chunks per stage
+  static constexpr int STAGE = (ACH + BCH) * 1024;
+  static constexpr int NB = AFMT == 0 ? 5 : 7;       // stage slots of the ring
+  static constexpr int AV = ACH / 4;                  // A loads per thread per stage
+  static constexpr int BV = BCH / 4;                  // weight loads per thread per stage
+  static constexpr int L = AV + BV;
+  // scales: one super-stage = 32 bytes per A row and per weight row, brought in by
+  // two 16-byte loads per row into registers once per 16 stages (the L2 requests,
+  // not the bytes, are what costs), double-buffered in LDS
+  static constexpr int SCL = 2 * kBM * kSPitch;
+  static constexpr int AS_OFF = NB * STAGE;
+  static constexpr int BS_OFF = AS_OFF + kBM * kSPitch;
+  static constexpr int LDS = NB * STAGE + 2 * SCL;
+  static_assert(LDS <= 160 * 1024, "the stage ring and two scale super-stages must fit the LDS");
+  static_assert(BCH == 8 && (ACH * 1024) == kBM * (AFMT == 0 ? kKS : kKS / 2), "chunking");
+};
+
+DSV4_DEV bool tiled_ptr(const uint8_t* p) { return ((uintptr_t)p & 1u) != 0; }
+DSV4_DEV const uint8_t* untag(const uint8_t* p) { return (const uint8_t*)((uintptr_t)p & ~(uintptr_t)1); }
+
+// 16 bytes per lane from src to dst + 16 * lane (dst: the same for the whole wave)
+DSV4_DEV void dma16(const uint8_t* src, uint8_t* dst) {
+  __builtin_amdgcn_global_load_lds((gvoid*)src, (lvoid*)dst, 16, 0, 0);
+}
+
+// Waits until at most N of this wave's vector-memory loads are outstanding, then
+// for every wave of the block. The direct-to-LDS loads are counted here by hand
+// (a workgroup fence would make the compiler drain them all at every barrier);
+// lgkmcnt(0) completes this wave's own LDS writes (the scales) first.
+// The wait is the s_waitcnt builtin rather than inline assembly so that the
+// compiler's own wait tracking sees it (it would otherwise keep counting the LDS
+// reads before it as pending); the empty asm statements keep memory accesses from
+// moving across the barrier.
+template <int N>
+DSV4_DEV void wait_loads_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  // simm16: vmcnt [3:0] and [15:14], expcnt [6:4] (7: no wait), lgkmcnt [11:8] (0)
+  constexpr int kEnc = (N & 15) | ((N >> 4) << 14) | (7 << 4);
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kEnc);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// one super-stage of scales for thread tid: A row tid's 32 bytes, weight row tid's 32 bytes
+struct BigScales {
+  v4i a[2], b[2];
+};
+
+DSV4_DEV void big_load_scales(BigScales& sc, const uint8_t* sa_src, const uint8_t* sb_src, int ss) {
+  sc.a[0] = *(gv4i*)(sa_src + ss * 32);
+  sc.a[1] = *(gv4i*)(sa_src + ss * 32 + 16);
+  sc.b[0] = *(gv4i*)(sb_src + ss * 32);
+  sc.b[1] = *(gv4i*)(sb_src + ss * 32 + 16);
+}
+
+template <int AFMT>
+DSV4_DEV void big_store_scales(const BigScales& sc, uint8_t* lds, int buf, int tid) {
+  using C = Big<AFMT>;
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  uint8_t* pa = lds + C::AS_OFF + buf * C::SCL + tid * kSPitch;
+  uint8_t* pb = lds + C::BS_OFF + buf * C::SCL + tid * kSPitch;
+  *(v2i*)(pa + 0) = v2i{sc.a[0].x, sc.a[0].y};
+  *(v2i*)(pa + 8) = v2i{sc.a[0].z, sc.a[0].w};
+  *(v2i*)(pa + 16) = v2i{sc.a[1].x, sc.a[1].y};
+  *(v2i*)(pa + 24) = v2i{sc.a[1].z, sc.a[1].w};
+  *(v2i*)(pb + 0) = v2i{sc.b[0].x, sc.b[0].y};
+  *(v2i*)(pb + 8) = v2i{sc.b[0].z, sc.b[0].w};
+  *(v2i*)(pb + 16) = v2i{sc.b[1].x, sc.b[1].y};
+  *(v2i*)(pb + 24) = v2i{sc.b[1].z, sc.b[1].w};
+}
+
+// Issues stage s's loads into ring slot `slot`: this wave's A chunks wave * AV + v and
+// weight chunks wave * BV + v (a_src / b_src: this lane's piece at stage 0; bj / bg:
+// the weight offset per 4 stages / per stage within them, no branch in the loop).
+template <int AFMT>
+DSV4_DEV void big_dma_stage(uint8_t* slot, const uint8_t* const* a_src, const uint8_t* const* b_src, int wave,
+                            int bj, int bg, int s) {
+  using C = Big<AFMT>;
+  const int aoff = s * (AFMT == 0 ? kKS : kKS / 2);
+#pragma unroll
+  for (int v = 0; v < C::AV; ++v) dma16(a_src[v] + aoff, slot + (wave * C::AV + v) * 1024);
+  // 4 stages = 256 k: 2048 bytes on in a tiled slot (128 row-major), 256 within it (32)
+  const int boff = (s >> 2) * bj + (s & 3) * bg;
+#pragma unroll
+  for (int v = 0; v < C::BV; ++v) dma16(b_src[v] + boff, slot + (C::ACH + wave * C::BV + v) * 1024);
+}
+
+// The fragments of one stage for this wave: weight tiles nt (16 bytes + scale each),
+// A tiles mt (E4M3: 2 x 16 bytes, E2M1: 16 bytes; + scale each).
+template <int AFMT>
+struct BigFrag {
+  v4i b[4];
+  v4i lo[4];
+  v4i hi[AFMT == 0 ? 4 : 1];
+  int sb[4], sa[4];
+};
+
+// Reads one stage's fragments from ring slot L. S: the scale super-stage buffer, q0:
+// this stage's first scale byte in it. a_lo / a_hi: this lane's byte offsets inside an
+// A chunk, b_lane inside a weight chunk.
+template <int AFMT>
+DSV4_DEV void big_read(BigFrag<AFMT>& F, const uint8_t* L, const uint8_t* S, int q0, int wm, const int* brow0,
+                       int r32, int g2, int a_lo, int a_hi, int b_lane) {
+  using C = Big<AFMT>;
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) {
+    F.b[nt] = *(const v4i*)(L + (C::ACH + brow0[nt] / 32) * 1024 + b_lane);
+    F.sb[nt] = S[kBM * kSPitch + (brow0[nt] + r32) * kSPitch + q0 + g2];
+  }
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int row0 = 128 * wm + 32 * mt;
+    if (AFMT == 0) {
+      const uint8_t* ch = L + (row0 / 16 + (r32 >> 4)) * 1024;
+      F.lo[mt] = *(const v4i*)(ch + a_lo);
+      F.hi[mt] = *(const v4i*)(ch + a_hi);
+    } else {
+      F.lo[mt] = *(const v4i*)(L + (row0 / 32) * 1024 + a_lo);
+    }
+    F.sa[mt] = S[(row0 + r32) * kSPitch + q0 + g2];
+  }
+}
+
+// Instruction order of one stage after its barrier: each MFMA (64 cycles in the
+// matrix pipe with FP8 A) followed by one of the stage's loads and two of the next
+// stage's fragment reads, so the LDS and the memory pipe work under the MFMAs and
+// the reads are done long before the next barrier waits for them.
+template <int AFMT>
+DSV4_DEV void big_sched() {
+  constexpr int kReads = AFMT == 0 ? 20 : 16;  // ds_reads of big_read
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA
+    if (i < Big<AFMT>::L) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+    if (2 * i < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);    // DS read
+  }
+}
+
+// One stage of MFMAs: 4 x 4 tiles of 32 x 32 per wave. The weights are the MFMA's A
+// operand and the activations its B operand, so accumulator (tt, wt) holds weight
+// columns x tokens: register r of lane l = weight column 8(r/4) + 4(l/32) + r%4 of
+// weight tile wt, token l%32 of token tile tt (the E4M3 B layout is the A layout).
+template <int AFMT>
+DSV4_DEV void big_mfma(v16f (&acc)[4][4], const BigFrag<AFMT>& F) {
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const v4i lo = F.lo[tt];
+    const v4i hi = AFMT == 0 ? F.hi[tt] : v4i{0, 0, 0, 0};
+    const v8i xf = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+    for (int wt = 0; wt < 4; ++wt) {
+      const v8i wf = v8i{F.b[wt].x, F.b[wt].y, F.b[wt].z, F.b[wt].w, 0, 0, 0, 0};
+      acc[tt][wt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf, xf, acc[tt][wt], 4, AFMT == 0 ? 0 : 4, 0,
+                                                                   F.sb[wt], 0, F.sa[tt]);
+    }
+  }
+}
+
+// ---- epilogue ---------------------------------------------------------------------
+// Each lane holds, per token tile tt, 4-column runs of one token's row (columns
+// 8q + 4(l/32) + e of every 32-column weight tile): SwiGLU, the quantisation blocks'
+// maxima (in-lane, then across the lane pair l, l ^ 32, then - FP8 h only - across the
+// two waves of a token row through the LDS) and the packing all stay in registers.
+// bf16 / E4M3 / E2M1 conversions use the gfx950 converters, which agree bit for bit
+// with the library's software quantisers on every input they see here (RNE; E4M3 after
+// the clamp to +-448; E2M1 with the sign of the input, whose -0 the rule-0 path
+// turns into +0 as that rule wants).
+
+// max of x over the lane pair (l, l ^ 32)
+DSV4_DEV float max_pair(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(x), __float_as_int(x), false, false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+
+// two floats -> packed bf16 (RNE), low half = a
+DSV4_DEV uint32_t pk_bf16(float a, float b) {
+  typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+  const v2bf v = v2bf{(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+DSV4_DEV float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+DSV4_DEV float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// silu(min(g, L)) * clamp(u, +-L) * w for bf16-rounded g, u; silu(g) = g / (1 + e^-g)
+// from the hardware exp2 and reciprocal (within an fp32 ulp or two of the correctly
+// rounded value, below the bf16 rounding of h that follows)
+DSV4_DEV float big_swiglu(float gt, float up, float w, float limit) {
+  if (limit > 0.0f) {
+    up = fminf(fmaxf(up, -limit), limit);
+    gt = fminf(gt, limit);
+  }
+  const float e = __builtin_amdgcn_exp2f(gt * -1.4426950408889634f);
+  return gt * __builtin_amdgcn_rcpf(1.0f + e) * up * w;
+}
+
+// 4 E4M3 codes of a * inv .. d * inv (inv = 2^-k), byte 0 = a
+DSV4_DEV uint32_t pk_fp8x4(float a, float b, float c, float d, float inv) {
+  const float m = 448.0f;
+  const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(fminf(fmaxf(a * inv, -m), m), fminf(fmaxf(b * inv, -m), m), 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(fminf(fmaxf(c * inv, -m), m), fminf(fmaxf(d * inv, -m), m), lo, true);
+}
+
+// E2M1 nibble pair of a * inv, b * inv (low nibble = a) under scale rule `rule`
+DSV4_DEV uint32_t pk_fp4x2(float a, float b, float inv, int rule) {
+  float ya = fminf(fmaxf(a * inv, -6.0f), 6.0f), yb = fminf(fmaxf(b * inv, -6.0f), 6.0f);
+  if (rule == 0) {  // the sign of a value that is exactly zero is +
+    ya = ya == 0.0f ? 0.0f : ya;
+    yb = yb == 0.0f ? 0.0f : yb;
+  }
+  return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, ya, yb, 1.0f, 0) & 0xffu;
+}
+
+// Block -> tile mapping. Workgroups are dispatched to the 8 XCDs round-robin by
+// linear id, and each XCD has its own L2, so with the plain mapping (N tiles fastest)
+// every XCD would run 2 of the 16 N tiles of every M block and fetch every M block's
+// A rows into its own L2. With N tiles a multiple of 8, the 32 consecutive
+// workgroups an XCD runs at once (one per CU) get 4 M blocks x 8 N tiles instead:
+// A rows shared 8 ways and weight tiles 4 ways within one L2. The grid's y extent
+// is then padded to a multiple of 32 M blocks; the padding blocks exit at once.
+DSV4_DEV void big_tile_of_block(int& mb, int& nt) {
+  const int ntiles = gridDim.x;
+  if (ntiles % 8 != 0) {
+    mb = blockIdx.y;
+    nt = blockIdx.x;
+    return;
+  }
+  const int id = blockIdx.y * ntiles + blockIdx.x;
+  const int x = id & 7, j = id >> 3;  // XCD, position in that XCD's sequence
+  const int gi = j >> 5, w = j & 31;  // group of 32, place in it
+  const int ngroups = ntiles >> 3;
+  mb = 4 * ((gi / ngroups) * 8 + x) + (w >> 3);
+  nt = 8 * (gi % ngroups) + (w & 7);
+}
+
+template <int AFMT, bool GATEUP>
+__global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
+  using C = Big<AFMT>;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[C::LDS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int mb, nt;
+  big_tile_of_block(mb, nt);
+  if (mb * kBM >= p.num_post_padded[0]) return;  // also every block of the grid's padding
+  const int e = p.block_expert[mb];
+  const Dsv4ExpertPtrs ex = p.experts[e];
+  const bool have_w = GATEUP ? (ex.w1p && ex.w1s && ex.w3p && ex.w3s) : (ex.w2p && ex.w2s);
+  const int NST = p.Kdim / kKS;
+  const int wrow_bytes = p.Kdim / 2, srow = p.Kdim / 32;
+  const int c0 = nt * (GATEUP ? 128 : 256);  // first intermediate column / output row of W2
+  const int slot0 = mb * kBM;
+
+  // this lane's A piece per A load (stage 0): chunk wave * AV + v
+  const uint8_t* a_src[C::AV];
+#pragma unroll
+  for (int v = 0; v < C::AV; ++v) {
+    const int c = wave * C::AV + v;
+    const int row = AFMT == 0 ? 16 * c + (lane >> 2) : 32 * c + (lane >> 1);
+    const int piece = AFMT == 0 ? (lane & 3) ^ ((lane >> 4) & 3) : (lane & 1) ^ ((lane >> 4) & 1);
+    const int f = p.sorted_ids[slot0 + row];
+    const int arow = f < p.R ? f / p.a_row_div : 0;  // padding rows read row 0 (never stored)
+    a_src[v] = p.a + (int64_t)arow * p.a_row_bytes + 16 * piece;
+  }
+  // this lane's weight piece per weight load: chunk wave * BV + v, slot `lane` =
+  // 16-row tile q / 32 of the block, 16-byte half (q / 16) % 2, row q % 16
+  const bool tiled = tiled_ptr(GATEUP ? ex.w1p : ex.w2p);
+  const int bj = tiled ? 2048 : 4 * (kKS / 2), bg = tiled ? 256 : kKS / 2;
+  const uint8_t* b_src[C::BV];
+#pragma unroll
+  for (int v = 0; v < C::BV; ++v) {
+    const int q = (wave * C::BV + v) * 64 + lane;
+    const int tile = q >> 5, ji = (q >> 4) & 1, r = q & 15;
+    const int gtile = c0 / 16 + (GATEUP ? (tile & 7) : tile);
+    const uint8_t* w = untag(GATEUP ? (tile < 8 ? ex.w1p : ex.w3p) : ex.w2p);
+    b_src[v] = w + (tiled ? (int64_t)((gtile * (p.Kdim / 256)) * 2 + ji) * 1024 + 16 * r
+                          : (int64_t)(16 * gtile + r) * wrow_bytes + 16 * ji);
+  }
+  const uint8_t* sa_src;
+  const uint8_t* sb_src;
+  {
+    const int f = p.sorted_ids[slot0 + tid];
+    const int arow = f < p.R ? f / p.a_row_div : 0;
+    sa_src = p.a_scale + (int64_t)arow * srow;
+    const uint8_t* ws = GATEUP ? (tid < 128 ? ex.w1s : ex.w3s) : ex.w2s;
+    sb_src = ws + (int64_t)(GATEUP ? c0 + (tid & 127) : c0 + tid) * srow;
+  }
+
+  v16f acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = v16f{};
+  const int r32 = lane & 31, g2 = lane >> 5;
+  // flat index (and gate/up: routing weight) of this lane's token in each token tile
+  int fr[4];
+  float wr[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    fr[tt] = p.sorted_ids[slot0 + 128 * wm + 32 * tt + r32];
+    wr[tt] = GATEUP && fr[tt] < p.R ? p.topk_w[fr[tt]] : 0.0f;
+  }
+  // first weight row of this wave's 32-row tile nt in the block
+  int brow0[4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt) brow0[nt] = GATEUP ? (nt >> 1) * 128 + 64 * wn + 32 * (nt & 1) : 128 * wn + 32 * nt;
+  // this lane's byte offsets inside a chunk (the swizzles of the layout comment)
+  int a_lo, a_hi;
+  if (AFMT == 0) {
+    const int r = r32 & 15, x = (r >> 2) & 3;
+    a_lo = 16 * (4 * r + (g2 ^ x));
+    a_hi = 16 * (4 * r + ((2 + g2) ^ x));
+  } else {
+    a_lo = 16 * (2 * r32 + (g2 ^ ((r32 >> 3) & 1)));
+    a_hi = 0;
+  }
+  const int b_lane = 16 * (32 * (r32 >> 4) + 16 * g2 + (r32 & 15));
+
+  if (have_w) {  // uniform per workgroup: every wave reaches every barrier
+    // Stage s lives in ring slot s % NB. Its fragments are read into registers during
+    // stage s - 1 (while stage s - 1's MFMAs run), so once the barrier at the top of
+    // stage s has passed - every wave holds its stage-s fragments - the slot takes the
+    // loads of stage s + NB. The wait before that barrier lands stage s + 1 and leaves
+    // the younger NB - 2 stages in flight. The loop has no branches (they would let
+    // the compiler move the MFMAs away from their stage): past the last stage the loads
+    // repeat stage NST - 1 into slots that are never read again, so every stage issues
+    // the same number of loads and the wait count stays exact. Scales: super-stage ss
+    // (stages 16ss..16ss+15) in LDS buffer ss % 2, written between stages 16ss - 1 and
+    // 16ss from registers loaded 16 stages earlier (past the end: a repeat of the last
+    // one into the buffer no stage reads). NST = K / 64 is a multiple of 16.
+    const int NSS = NST / kSS;
+    BigScales sc;
+    big_load_scales(sc, sa_src, sb_src, 0);
+#pragma unroll
+    for (int t = 0; t < C::NB; ++t) big_dma_stage<AFMT>(lds + t * C::STAGE, a_src, b_src, wave, bj, bg, t);
+    big_store_scales<AFMT>(sc, lds, 0, tid);
+    big_load_scales(sc, sa_src, sb_src, min(1, NSS - 1));
+    wait_loads_barrier<C::L * (C::NB - 1)>();
+    BigFrag<AFMT> f0, f1;
+    big_read<AFMT>(f0, lds, lds + C::AS_OFF, 0, wm, brow0, r32, g2, a_lo, a_hi, b_lane);
+    int slot = 0;  // ring slot of stage s
+    // stage s: multiply Fc (stage s), read stage s + 1 into Fn
+#define DSV4_BIG_STEP(Fc, Fn)                                                                                  \
+  {                                                                                                            \
+    const int nslot = slot + 1 == C::NB ? 0 : slot + 1;                                                        \
+    wait_loads_barrier<C::L * (C::NB - 2)>();                                                                  \
+    big_dma_stage<AFMT>(lds + slot * C::STAGE, a_src, b_src, wave, bj, bg, min(s + C::NB, NST - 1));            \
+    const int s1 = s + 1;                                                                                      \
+    big_read<AFMT>(Fn, lds + nslot * C::STAGE, lds + C::AS_OFF + ((s1 / kSS) & 1) * C::SCL, 2 * (s1 % kSS),   \
+                   wm, brow0, r32, g2, a_lo, a_hi, b_lane);                                                    \
+    big_mfma<AFMT>(acc, Fc);                                                                                   \
+    big_sched<AFMT>();                                                                                         \
+    slot = nslot;                                                                                              \
+  }
+#pragma unroll 1
+    for (int ss = 0; ss < NSS; ++ss) {
+      big_store_scales<AFMT>(sc, lds, (ss + 1) & 1, tid);
+      big_load_scales(sc, sa_src, sb_src, min(ss + 2, NSS - 1));
+#pragma unroll 1
+      for (int s = kSS * ss; s < kSS * (ss + 1); ++s) {
+        DSV4_BIG_STEP(f0, f1);
+        ++s;
+        DSV4_BIG_STEP(f1, f0);
+      }
+    }
+#undef DSV4_BIG_STEP
+  }
+  wait_loads_barrier<0>();  // every wave is done with the ring
+
+  // epilogue (every wave is past the ring: the LDS is free)
+  if (GATEUP) {
+    const int cw = c0 + 64 * wn;  // this wave's first intermediate column
+    // h for columns cw + 32 h2 + 8 q + 4 g2 + e of token tile tt, packed bf16 pairs
+    uint32_t hp[4][2][4][2];
+    float rmax[4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      float m = 0.0f;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; e += 2) {
+            const int r = 4 * q + e;
+            // gate (tile h2) and up (tile h2 + 2) of the same column, rounded to bf16
+            const uint32_t gu0 = pk_bf16(acc[tt][h2][r], acc[tt][h2 + 2][r]);
+            const uint32_t gu1 = pk_bf16(acc[tt][h2][r + 1], acc[tt][h2 + 2][r + 1]);
+            const uint32_t hw = pk_bf16(big_swiglu(bf16_lo(gu0), bf16_hi(gu0), wr[tt], p.swiglu_limit),
+                                        big_swiglu(bf16_lo(gu1), bf16_hi(gu1), wr[tt], p.swiglu_limit));
+            hp[tt][h2][q][e >> 1] = hw;
+            m = fmaxf(m, fmaxf(fabsf(bf16_lo(hw)), fabsf(bf16_hi(hw))));
+          }
+      rmax[tt] = m;
+    }
+    if (!p.hq_skip_h && p.out) {
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+        if (fr[tt] < p.R)
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+              *(v2u*)(p.out + (int64_t)fr[tt] * p.N + cw + 32 * h2 + 8 * q + 4 * g2) =
+                  v2u{hp[tt][h2][q][0], hp[tt][h2][q][1]};
+            }
+    }
+    if (p.hq_mode == 2) {  // MXFP4 h: one 32-column block per (tt, h2), half of it in each lane of a pair
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int h2 = 0; h2 < 2; ++h2) {
+          float m = 0.0f;
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+              const uint32_t w = hp[tt][h2][q][j];
+              m = fmaxf(m, fmaxf(fabsf(bf16_lo(w)), fabsf(bf16_hi(w))));
+            }
+          const int k = dsv4::mxfp4_block_exp(max_pair(m), p.hq_rule);
+          const float inv = dsv4::pow2f(-k);
+          if (fr[tt] < p.R) {
+            const int col = cw + 32 * h2;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t w0 = hp[tt][h2][q][0], w1 = hp[tt][h2][q][1];
+              const uint32_t nib = pk_fp4x2(bf16_lo(w0), bf16_hi(w0), inv, p.hq_rule) |
+                                   pk_fp4x2(bf16_lo(w1), bf16_hi(w1), inv, p.hq_rule) << 8;
+              *(uint16_t*)(p.hq_codes + (int64_t)fr[tt] * (p.N / 2) + (col + 8 * q + 4 * g2) / 2) = (uint16_t)nib;
+            }
+            if (g2 == 0) p.hq_scale[(int64_t)fr[tt] * (p.N / 32) + col / 32] = (uint8_t)(k + 127);
+          }
+        }
+    } else if (p.hq_mode == 1) {  // FP8 h: one 128-column block per token, split over the wn pair of waves
+      float* am = (float*)lds;     // [2 wn][256 rows]
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        rmax[tt] = max_pair(rmax[tt]);
+        if (g2 == 0) am[wn * 256 + 128 * wm + 32 * tt + r32] = rmax[tt];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const int k = dsv4::fp8_block_exp(fmaxf(rmax[tt], am[(1 - wn) * 256 + 128 * wm + 32 * tt + r32]));
+        const float inv = dsv4::pow2f(-k);
+        if (fr[tt] < p.R) {
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t w0 = hp[tt][h2][q][0], w1 = hp[tt][h2][q][1];
+              *(uint32_t*)(p.hq_codes + (int64_t)fr[tt] * p.N + cw + 32 * h2 + 8 * q + 4 * g2) =
+                  pk_fp8x4(bf16_lo(w0), bf16_hi(w0), bf16_lo(w1), bf16_hi(w1), inv);
+            }
+          if (g2 == 0) *(uint16_t*)(p.hq_scale + (int64_t)fr[tt] * (p.N / 32) + cw / 32) = (uint16_t)((k + 127) * 0x0101);
+        }
+      }
+    }
+  } else {
+    const int cw = c0 + 128 * wn;  // this wave's first output column
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+      if (fr[tt] < p.R)
+#pragma unroll
+        for (int wt = 0; wt < 4; ++wt)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+            const int r = 4 * q;
+            *(v2u*)(p.out + (int64_t)fr[tt] * p.N + cw + 32 * wt + 8 * q + 4 * g2) =
+                v2u{pk_bf16(acc[tt][wt][r], acc[tt][wt][r + 1]), pk_bf16(acc[tt][wt][r + 2], acc[tt][wt][r + 3])};
+          }
+  }
+}
+
+}  // namespace
+
+// K in whole 1024-k scale super-stages (the K = 512 GEMMs keep the 64-row kernel).
+bool moe_gemm_big_supported(int kdim, int n, bool gateup) {
+  return kdim >= 1024 && kdim % 1024 == 0 && n % (gateup ? 128 : 256) == 0;
+}
+
+hipError_t launch_moe_gemm_big(const Dsv4GemmArgs& a, bool gateup, hipStream_t st) {
+  if (a.block_m != kBM || !moe_gemm_big_supported(a.Kdim, a.N, gateup)) return hipErrorInvalidValue;
+  if (a.max_blocks <= 0) return hipSuccess;
+  const int ntiles = a.N / (gateup ? 128 : 256);
+  // the XCD grouping of big_tile_of_block needs M blocks in whole groups of 32
+  const int mblocks = ntiles % 8 == 0 ? (a.max_blocks + 31) / 32 * 32 : a.max_blocks;
+  const dim3 grid(ntiles, mblocks);
+  if (gateup) {
+    if (a.afmt == 0) hipLaunchKernelGGL((moe_gemm_big_kernel<0, true>), grid, dim3(kNT), 0, st, a);
+    else hipLaunchKernelGGL((moe_gemm_big_kernel<1, true>), grid, dim3(kNT), 0, st, a);
+  } else {
+    if (a.afmt == 0) hipLaunchKernelGGL((moe_gemm_big_kernel<0, false>), grid, dim3(kNT), 0, st, a);
+    else hipLaunchKernelGGL((moe_gemm_big_kernel<1, false>), grid, dim3(kNT), 0, st, a);
+  }
+  return hipGetLastError();
+}

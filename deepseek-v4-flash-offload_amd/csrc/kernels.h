@@ -52,13 +52,26 @@ hipError_t launch_moe_align_quant(const void* topk_ids, int ids_int64, const flo
                                   int block_m, int max_blocks, const Dsv4AlignOut& o, const uint16_t* x,
                                   int64_t n_elems, int qfmt, int rule, void* q_codes, void* q_scale,
                                   hipStream_t st, int n_shared = 0);
+// Second padded layout for experts with many rows: every expert with at least
+// hot_min routed entries is laid out here in blocks of kHotBlockM rows (and gets
+// no blocks in the main layout). hot_min = 0: none.
+constexpr int kHotBlockM = 256;
+struct Dsv4AlignHot {
+  int hot_min;
+  int max_blocks;
+  int32_t* sorted_ids;       // [max_blocks * kHotBlockM]
+  int32_t* block_expert;     // [max_blocks]
+  int32_t* num_post_padded;  // [1]
+};
 // The same outputs from two launches for many entries: per-chunk counts (plus
 // the quantisation of x when x is non-null), then per-chunk layout + scatter. scratch: align_chunked_scratch_bytes(R, E) bytes of device memory.
+// hot (nullable): also the hot layout; the main layout's padded_pos then holds
+// -1 - (hot position) for the hot experts' entries and expert_start -1 for them.
 int64_t align_chunked_scratch_bytes(int R, int E);
 hipError_t launch_moe_align_chunked(const void* topk_ids, int ids_int64, const float* topk_w, int R, int K, int E,
                                     int block_m, int max_blocks, const Dsv4AlignOut& o, const uint16_t* x,
                                     int64_t n_elems, int qfmt, int rule, void* q_codes, void* q_scale,
-                                    hipStream_t st, int n_shared, void* scratch);
+                                    hipStream_t st, int n_shared, void* scratch, const Dsv4AlignHot* hot = nullptr);
 hipError_t launch_moe_gather_rows(const uint8_t* src, int64_t n_src, const int32_t* row, int64_t n_rows,
                                   int64_t row_bytes, uint8_t* dst, hipStream_t st);
 // y[t] = bf16( sum over the token's entries, ordered by key, of rows of `src` (bf16) )
@@ -113,8 +126,12 @@ struct Dsv4GemmArgs {
 };
 hipError_t launch_moe_gemm_gateup(const Dsv4GemmArgs& a, hipStream_t st);
 hipError_t launch_moe_gemm_down(const Dsv4GemmArgs& a, hipStream_t st);
+// The large-tile kernel over a hot layout (block_m = kHotBlockM; no shared expert):
+// gate/up (with the same epilogue options) or down.
+bool moe_gemm_big_supported(int kdim, int n, bool gateup);
+hipError_t launch_moe_gemm_big(const Dsv4GemmArgs& a, bool gateup, hipStream_t st);
 bool moe_gemm_supported_kdim(int kdim);  // reduction lengths with a compiled kernel (512..4096, powers of two)
-bool moe_gemm_supported_block_m(int bm);  // 16 (decode kernel), 64 or 128 (tiled kernel)
+bool moe_gemm_supported_block_m(int bm);  // 16 (decode kernel), 64 or 128 (tiled kernel), 256 (large-tile kernel)
 
 // Router top-k of one layer (per-token arguments of route_topk_token).
 struct RouteTopkArgs {

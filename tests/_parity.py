@@ -49,16 +49,17 @@ def swiglu_bound(g, u, w, limit, h, g_abs_sum=None, u_abs_sum=None, acc_rel=ACC_
     g = np.asarray(g, np.float64)
     u = np.asarray(u, np.float64)
     w = np.asarray(w, np.float64)[:, None]
-    gc = np.minimum(g, limit) if limit else g
-    uc = np.clip(u, -limit, limit) if limit else u
-    sig = 1.0 / (1.0 + np.exp(-gc))
-    dsilu = sig * (1.0 + gc * (1.0 - sig))
-    dh_dg = np.abs(w * uc * dsilu) * ((g < limit) if limit else 1.0)
-    dh_du = np.abs(w * gc * sig) * ((np.abs(u) < limit) if limit else 1.0)
     fg = floor_frac * max(np.abs(g).max(), 1e-30)
     fu = floor_frac * max(np.abs(u).max(), 1e-30)
     eg = bf16_ulp(np.maximum(np.abs(g), fg)) + (0.0 if g_abs_sum is None else acc_rel * np.asarray(g_abs_sum))
     eu = bf16_ulp(np.maximum(np.abs(u), fu)) + (0.0 if u_abs_sum is None else acc_rel * np.asarray(u_abs_sum))
+    gc = np.minimum(g, limit) if limit else g
+    uc = np.clip(u, -limit, limit) if limit else u
+    sig = 1.0 / (1.0 + np.exp(-gc))
+    dsilu = sig * (1.0 + gc * (1.0 - sig))
+    # a value within its own error of the clamp may land on either side of it
+    dh_dg = np.abs(w * uc * dsilu) * ((g - eg < limit) if limit else 1.0)
+    dh_du = np.abs(w * gc * sig) * ((np.abs(u) - eu < limit) if limit else 1.0)
     return ulp_bound(h, 1.0, floor_frac) + dh_dg * eg + dh_du * eu
 
 

@@ -67,9 +67,12 @@ def _case(T, K, E, D, I, seed, dev):
 @pytest.mark.parametrize("profile", ["bf16", "a4w4"])
 @pytest.mark.parametrize("T,K,E,D,I,bm", [(24, 4, 16, 1024, 512, 16), (200, 8, 16, 512, 512, 16),
                                           (8, 8, 256, 4096, 2048, 16), (200, 8, 16, 512, 512, 64),
-                                          (200, 8, 16, 1024, 512, 128), (300, 6, 24, 2048, 1024, 64)])
+                                          (200, 8, 16, 1024, 512, 128), (300, 6, 24, 2048, 1024, 64),
+                                          (200, 8, 16, 1024, 1024, 256), (300, 6, 24, 2048, 1024, 256),
+                                          (640, 8, 8, 4096, 2048, 256)])
 def test_grouped_gemm_stages(gpu, profile, T, K, E, D, I, bm):
-    # bm 16 runs the single-wave decode kernel, 64/128 the LDS-tiled kernel
+    # bm 16 runs the single-wave decode kernel, 64/128 the LDS-tiled kernel, 256 the
+    # large-tile kernel (256 x 256 workgroup tiles, 32x32x64 MFMA)
     ids, w, xb, host, devw, table = _case(T, K, E, D, I, 31 + T, gpu)
     al = ops.moe_align(_dev(ids, gpu), _dev(w, gpu), E, bm)
     R = T * K
