@@ -50,7 +50,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default="",
-                    help="profile helper: run only 'decode', 'dequant', 'prefill', 'router', 'routed', 'shared' or 'offload'")
+                    help="profile helper: run only 'decode', 'dequant', 'prefill', 'prefill2048', 'compute', "
+                         "'router', 'routed', 'shared', 'offload' or 'cpu' (CPU baselines of configs 0, 2, 3, 4)")
     ap.add_argument("--offload-steps", type=int, default=512, help="decode steps of the expert-offload leg")
     ap.add_argument("--weight-layout", choices=("tiled", "checkpoint"), default="tiled",
                     help="packed expert weights in HBM: the MFMA-tiled layout (default) or the checkpoint layout")
@@ -444,6 +445,93 @@ def cpu_baseline(sample_steps=2, threads=None, min_seconds=10.0):
                       f"{dt:.2f} s/step"}
 
 
+def _timed(fn, min_seconds, min_runs=1, warmup=True):
+    """Calls fn until min_runs calls and min_seconds have passed; (seconds per call, calls)."""
+    if warmup:
+        fn()
+    t0 = time.perf_counter()
+    n = 0
+    while n < min_runs or time.perf_counter() - t0 < min_seconds:
+        fn()
+        n += 1
+    return (time.perf_counter() - t0) / n, n
+
+
+def cpu_baselines(threads=None, seconds=8.0):
+    """The numpy oracle of configs 0, 2, 3 and 4 on the host cores (reported baselines;
+    config 1 is ``cpu_baseline``). Each is a bounded sample: a few calls after one
+    warm-up, experts spread over ``threads`` threads with single-threaded BLAS inside."""
+    import platform
+    from threadpoolctl import threadpool_limits
+    from oracle import moe as M
+    from oracle import mxfp4 as Q
+    from oracle.lru import LRUOracle
+    from dsv4_hip import synth
+    threads = threads or min(os.cpu_count() or 1, 16)
+    cpu_model = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), cpu_model)
+    except OSError:
+        pass
+    out = {"threads": threads, "host_cores": os.cpu_count(), "cpu_model": cpu_model,
+           "torch": torch.__version__, "numpy": np.__version__, "kind": "port"}
+    with threadpool_limits(limits=1):
+        # config 0: one [2048, 4096] MXFP4 matrix -> bf16, and the bf16 GEMV x [1, 4096] @ W^T
+        packed, scales, x = synth.dequant_config0()
+        xb = x.view(torch.int16).numpy().view(np.uint16)
+        t_dq, n_dq = _timed(lambda: Q.dequant_fp4_weight(packed, scales), seconds / 2)
+        t_gv, n_gv = _timed(lambda: M.dequant_gemv(xb, packed, scales), seconds / 2)
+        out["config0_dequant_gemv"] = {"dequant_gbs": 2048 * 4096 * 2.53125 / t_dq / 1e9, "dequant_ms": t_dq * 1e3,
+                                       "gemv_with_dequant_ms": t_gv * 1e3, "sample": f"{n_dq} dequants, {n_gv} GEMVs"}
+        # config 2: a4w4 layer, 64 tokens
+        x2, ids2, w2 = synth.layer_inputs(64, 8, E, D)
+        xb2 = x2.view(torch.int16).numpy().view(np.uint16)
+        ex2 = {int(e): synth.expert_weights(int(e), D, I) for e in np.unique(ids2)}
+        t2, n2 = _timed(lambda: M.routed_a4w4(xb2, ids2, w2, ex2, n_experts=E, workers=threads), seconds,
+                        warmup=False)
+        out["config2_a4w4_64"] = {"tokens_per_s": 64 / t2, "ms_per_layer": t2 * 1e3,
+                                  "sample": f"{n2} layer calls, {len(ex2)} active experts"}
+        # config 3: prefill, 2048 tokens, both profiles (one call each, ~15-30 s of CPU work)
+        x3, ids3, w3 = synth.layer_inputs(2048, 8, E, D)
+        xb3 = x3.view(torch.int16).numpy().view(np.uint16)
+        ex3 = {int(e): synth.expert_weights(int(e), D, I) for e in np.unique(ids3)}
+        flops3 = 6.0 * 2048 * 8 * D * I
+        for name, fn in (("config3_bf16_2048", lambda: M.routed_bf16(xb3, ids3, w3, ex3, n_experts=E, workers=threads)),
+                         ("config3_a4w4_2048", lambda: M.routed_a4w4(xb3, ids3, w3, ex3, n_experts=E,
+                                                                    workers=threads))):
+            t3, n3 = _timed(fn, 0.0, warmup=False)
+            out[name] = {"tokens_per_s": 2048 / t3, "ms_per_layer": t3 * 1e3, "tflops": flops3 / t3 / 1e12,
+                         "sample": f"{n3} layer call(s), {len(ex3)} active experts"}
+        del ex3
+        # config 4: the offload workload's routing (8 layers, drifting Zipf, 512 slots) through
+        # an LRU of packed experts; on the host every layer dequantises its active experts
+        route = synth.DriftingZipf(8, E, 8)
+        lru = LRUOracle(512)
+        bases = [synth.expert_weights(e, D, I) for e in range(8)]
+        wts = synth.routing_weights(8, 8, 1000)
+        xb4 = synth.bf16_normal(np.random.default_rng(6), (8, D)).view(torch.int16).numpy().view(np.uint16)
+        for _ in range(64):                  # warm the LRU with the bench's own warm-up steps
+            for l, ids in enumerate(route.step(8)):
+                for e in np.unique(ids):
+                    lru.access((l, int(e)))
+        lru.hits = lru.misses = lru.evictions = 0
+        n_layers, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds or n_layers < 8:
+            for l, ids in enumerate(route.step(8)):
+                for e in np.unique(ids):
+                    lru.access((l, int(e)))
+                ex = {int(e): bases[(l * 7 + int(e)) % 8] for e in np.unique(ids)}
+                M.routed_bf16(xb4, ids, wts, ex, n_experts=E, workers=threads)
+                n_layers += 1
+        t4 = (time.perf_counter() - t0) / n_layers
+        out["config4_offload"] = {"layer_tokens_per_s": 8 / t4, "ms_per_layer": t4 * 1e3,
+                                  "hit_rate": lru.stats()["hit_rate"],
+                                  "sample": f"{n_layers} layer calls (8 tokens each) of the drifting-Zipf routing "
+                                            "after 64 warm-up steps; every active expert dequantised per call"}
+    return out
+
+
 def main():
     global WEIGHT_LAYOUT
     args = parse()
@@ -508,12 +596,19 @@ def main():
     if not args.no_extra and args.only in ("", "dequant"):
         extra["dequant_config0"] = measure_dequant(dev, gen)
         torch.cuda.empty_cache()
-    if not args.no_extra and args.only in ("", "prefill"):
+    if not args.no_extra and args.only in ("", "prefill", "prefill2048", "compute"):
         pools, tables = gen_layer_weights(dev, 2, gen)
         runner = ops.LayerRunner(dev, E, D, I)
-        for name, Tn, prof in (("a4w4_decode_64", 64, PROFILE_A4W4), ("bf16_prefill_2048", 2048, PROFILE_BF16),
-                               ("a4w4_prefill_2048", 2048, PROFILE_A4W4)):
-            host = routing_batches(4, Tn, K, 21 + Tn)
+        legs = []
+        if args.only in ("", "prefill", "prefill2048"):
+            legs += [("a4w4_decode_64", 64, PROFILE_A4W4), ("bf16_prefill_2048", 2048, PROFILE_BF16),
+                     ("a4w4_prefill_2048", 2048, PROFILE_A4W4)]
+        if args.only in ("", "prefill", "compute"):
+            # the compute-bound point: 16384 tokens x top-8 = 131072 routed rows, every expert
+            # with hundreds of rows, arithmetic intensity ~1.9 kFLOP/B (MXFP4 ridge ~1.26 kFLOP/B)
+            legs += [("bf16_prefill_16384", 16384, PROFILE_BF16), ("a4w4_prefill_16384", 16384, PROFILE_A4W4)]
+        for name, Tn, prof in legs:
+            host = routing_batches(2 if Tn > 2048 else 4, Tn, K, 21 + Tn)
             dev_b = [(x.to(dev), torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(dev))
                      for x, ids, w in host]
             st = 20 if Tn <= 64 else 5
@@ -523,9 +618,11 @@ def main():
             byts = A * EXPERT_BYTES + 4 * Tn * D
             peak = MXFP4_PEAK_TFLOPS if prof == PROFILE_A4W4 else FP8_PEAK_TFLOPS
             extra[name] = {"ms_per_layer": s2 * 1e3, "tokens_per_s": Tn / s2, "tflops": flops / s2 / 1e12,
-                           "frac_mfma_peak": flops / s2 / 1e12 / peak, "hbm_gbs": byts / s2 / 1e9,
-                           "frac_hbm": byts / s2 / 1e9 / HBM_PEAK_GBS, "active_experts": A}
-        del pools, tables
+                           "frac_mfma_peak": flops / s2 / 1e12 / peak, "mfma_peak_tflops": peak,
+                           "hbm_gbs": byts / s2 / 1e9, "frac_hbm": byts / s2 / 1e9 / HBM_PEAK_GBS,
+                           "active_experts": A}
+            del host, dev_b
+        del pools, tables, runner
         torch.cuda.empty_cache()
     if not args.no_extra and args.only in ("", "router"):
         extra["router"] = measure_router(dev)
@@ -540,6 +637,9 @@ def main():
     if not args.no_cpu_baseline and args.only == "":
         line["cpu_baseline"] = cpu_baseline()
         line["cpu_baseline"]["host_threads_available"] = os.cpu_count()
+    if not args.no_cpu_baseline and args.only in ("", "cpu"):
+        extra["cpu_baselines"] = cpu_baselines()
+        line["extra"] = extra
     print(json.dumps(line), flush=True)
 
 

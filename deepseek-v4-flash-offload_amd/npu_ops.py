@@ -125,16 +125,25 @@ def moe_unpermute(out: torch.Tensor, row: torch.Tensor, num_tokens: int) -> torc
 
 
 def grouped_matmul(x, weight, group_list, scale=None, per_token_scale=None, group_list_type=1,
-                   output_dtype=torch.bfloat16, **unused):
+                   output_dtype=torch.bfloat16, fp8_roundtrip=False, **unused):
     """Grouped ``x_g @ W_g^T`` over consecutive row groups, for MXFP4 weights.
 
     Keyword form of ``npu_grouped_matmul`` (``deepseek_v4.py:177-193,224-229``):
     ``x=[x]``, ``weight=[...]`` per-group packed ``[N, K/2]`` (or the
     reference's stacked ``[g, K/2, N]`` transposed view), ``scale=[...]`` their
     ``[N, K/32]`` E8M0, ``group_list`` per-group row counts
-    (``group_list_type=1``). Activations are either packed E2M1 ``[M, K/2]``
-    with ``per_token_scale=[[M, K/32]]`` (a4w4) or bf16 ``[M, K]`` (quantised
-    here with the FP8 round trip of the bf16 profile). Output bf16 ``[M, N]``."""
+    (``group_list_type=1``). Output bf16 ``[M, N]``. Activations:
+
+    * packed E2M1 ``[M, K/2]`` with ``per_token_scale=[[M, K/32]]`` (a4w4,
+      ``deepseek_v4.py:224-229``);
+    * bf16 ``[M, K]`` with ``fp8_roundtrip=True``: x is first replaced by its
+      per-128 FP8 round trip (``act_quant(x, 128, "ue8m0", None, True)``), as
+      the bf16 profile does before each of its grouped GEMMs
+      (``deepseek_v4.py:170,188``), and the product runs on the FP8 x FP4 MFMA.
+
+    A plain bf16 x (``npu_grouped_matmul(x=[bf16], weight=[bf16 w.t()])``)
+    without ``fp8_roundtrip`` raises: this entry point does not compute a
+    bf16 x bf16 product, and quantising x silently would change the numbers."""
     if group_list_type != 1:
         raise NotImplementedError("grouped_matmul: group_list_type=1 (counts) only")
     if output_dtype != torch.bfloat16:
@@ -170,6 +179,11 @@ def grouped_matmul(x, weight, group_list, scale=None, per_token_scale=None, grou
         xsc = xsc.reshape(M, K // 32).view(torch.uint8).contiguous()
         afmt = _lib.AFMT_E2M1
     else:
+        if xs.dtype != torch.bfloat16 or not fp8_roundtrip:
+            raise NotImplementedError(
+                "grouped_matmul: activations must be packed E2M1 with per_token_scale, or bf16 with "
+                "fp8_roundtrip=True (the bf16 profile's per-128 FP8 round trip); a bf16 x bf16 product is "
+                f"not computed here (x dtype {xs.dtype})")
         q = _ops.fp8_act_quant(xs.contiguous(), 128, want_codes=True, want_e8m0x4=True)
         xa, xsc, afmt = q["codes"], q["e8m0x4"], _lib.AFMT_E4M3
     return _ops.gemm_down(afmt, xa, xsc, al, table, K, N)

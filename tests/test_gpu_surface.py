@@ -117,8 +117,11 @@ def test_npu_ops_grouped_matmul_groups_2_0_3(gpu, form):
     if form == "bf16_x":
         rt = Q.act_quant(xb, 128)[0]
         a_f = Q.bf16_bits_to_f32(rt)
-        out = npu_ops.grouped_matmul(x=[x.to(gpu)], weight=[torch.from_numpy(w).to(gpu) for w, _ in wts],
-                                     scale=[torch.from_numpy(s).to(gpu) for _, s in wts], group_list=counts)
+        kw = dict(weight=[torch.from_numpy(w).to(gpu) for w, _ in wts],
+                  scale=[torch.from_numpy(s).to(gpu) for _, s in wts], group_list=counts)
+        with pytest.raises(NotImplementedError, match="fp8_roundtrip"):
+            npu_ops.grouped_matmul(x=[x.to(gpu)], **kw)          # no silent FP8 quantisation of bf16 x
+        out = npu_ops.grouped_matmul(x=[x.to(gpu)], fp8_roundtrip=True, **kw)
     else:
         _, xp, xs = Q.ocp_mx_quant(xb, 32)
         a_f = Q.fp4_codes_to_f32(xp, xs)
