@@ -363,8 +363,14 @@ struct LayerWs {
 };
 
 // Experts with at least this many routed rows run in 256-row blocks on the
-// large-tile kernel once the chunked align is in use (above 2048 routed rows);
-// the rest keep 64-row blocks. DSV4_HOT_ROWS overrides it (0: never), read once.
+// large-tile kernel in layers of at least kHotLayerRows routed rows; the rest keep
+// 64-row blocks. DSV4_HOT_ROWS overrides it (0: never), read once.
+// Below this many routed rows (8192 tokens at top-8) the hot experts' blocks are too
+// few to fill a launch of their own: measured with Zipf(1.1) routing over 256 experts
+// (hidden 4096, inter 2048), the two-launch split lost 2-10% at 2048-6144 tokens and
+// gained 2% at 8192, 5% at 12288 and 7-10% at 16384.
+constexpr int64_t kHotLayerRows = 65536;
+
 static int hot_rows_threshold() {
   static const int v = [] {
     const char* s = getenv("DSV4_HOT_ROWS");
@@ -404,7 +410,8 @@ static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool sha
   w.align_scratch = R > kAlignSmallRows ? take(align_chunked_scratch_bytes((int)R, E)) : 0;
   w.route_part = routed ? take(dsv4_moe_route_workspace_bytes(T, D, E)) : -1;  // router partial logits
   const int hot = hot_rows_threshold();
-  if (R > kAlignSmallRows && hot > 0 && moe_gemm_big_supported(D, I, true) && moe_gemm_big_supported(I, D, false)) {
+  if (R >= kHotLayerRows && R > kAlignSmallRows && hot > 0 && moe_gemm_big_supported(D, I, true) &&
+      moe_gemm_big_supported(I, D, false)) {
     w.hot_min = hot;
     // each hot expert holds >= hot_min rows: blocks <= R/256 + min(E, R/hot_min) + 1
     w.max_blocks_h = (int)(R / kHotBlockM + std::min<int64_t>(E, R / hot) + 1);

@@ -7,12 +7,16 @@ against the oracle run on a few of its tokens. Sizes: 256 experts, top-8,
 hidden 4096, inter 2048, at
 * 2048 tokens in both profiles: 16,384 routed rows, 64-row blocks, the chunked
   align, Zipf-hot experts spread over dozens of blocks;
+* 16384 tokens in both profiles: 131,072 routed rows; experts with at least 256
+  rows (the Zipf-hot ones, up to ~14,000 rows) run in 256-row blocks on the
+  large-tile kernel, the others in 64-row blocks;
 * 64 tokens in the a4w4 profile: 512 routed rows on the 16-row kernel.
 Expert weights are random bytes generated on the device and stored MFMA-tiled,
 as the slot cache stores them. The oracle reads checkpoint-layout copies of the
 sampled tokens' experts. The sample at 2048 tokens: the tokens of the first and
 last routed row of every M block of the 16 hottest experts (the block edges of
-every hot expert; ~260 tokens) plus 32 random ones; at 64 tokens, all of them.
+every hot expert; ~260 tokens) plus 32 random ones; at 16384 tokens the same for
+the 8 hottest experts in their 256-row blocks; at 64 tokens, all of them.
 Tolerances: max relative error (normwise) 1e-2 for bf16, 2e-2 for a4w4; per
 element, bf16 within 5e-2 of max(|ref|, rms(ref)) and a4w4 bit for bit."""
 
@@ -49,7 +53,8 @@ def _device_experts(dev, seed):
     return ex
 
 
-@pytest.mark.parametrize("profile,T", [("bf16", 2048), ("a4w4", 2048), ("a4w4", 64)])
+@pytest.mark.parametrize("profile,T", [("bf16", 2048), ("a4w4", 2048), ("a4w4", 64), ("bf16", 16384),
+                                       ("a4w4", 16384)])
 def test_full_size_layer_on_sampled_tokens(gpu, profile, T):
     ids = synth.zipf_topk(T, K, E, synth.rank_permutation(E, 3), np.random.default_rng(T))
     w = synth.routing_weights(T, K, T + 1)
@@ -87,17 +92,20 @@ def test_full_size_layer_on_sampled_tokens(gpu, profile, T):
 def _sample_tokens(ids, T, n_hot=16, n_random=32):
     """Tokens of the first and last routed row of every M block of the n_hot
     hottest experts (rows of an expert in flat-index order, blocks of the
-    layer's block size: 64 rows from 2048 routed rows on, else 16), plus
-    n_random random tokens; every token when T <= 64."""
+    layer's block size: 64 rows from 2048 routed rows on, else 16; 256 for
+    experts with at least 256 rows from 65,536 routed rows on, where only the
+    8 hottest are taken), plus n_random random tokens; every token when T <= 64."""
     if T <= 64:
         return np.arange(T)
     R = ids.size
-    bm = 64 if R >= 2048 else 16
     flat = ids.reshape(-1)
     counts = np.bincount(flat, minlength=E)
     picks = set()
+    if R >= 65536:  # the layer's large-tile split: 256-row blocks for experts with >= 256 rows
+        n_hot = 8
     for e in np.argsort(-counts, kind="stable")[:n_hot]:
         tok = np.nonzero(flat == e)[0] // ids.shape[1]
+        bm = 256 if (R >= 65536 and tok.size >= 256) else (64 if R >= 2048 else 16)
         for b in range(0, tok.size, bm):
             picks.add(int(tok[b]))
             picks.add(int(tok[min(b + bm, tok.size) - 1]))
