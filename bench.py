@@ -51,7 +51,8 @@ def parse():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--only", default="",
                     help="profile helper: run only 'decode', 'dequant', 'prefill', 'prefill2048', 'compute', "
-                         "'router', 'routed', 'shared', 'offload' or 'cpu' (CPU baselines of configs 0, 2, 3, 4)")
+                         "'router', 'routed', 'shared', 'offload', 'mfma' (matrix-core issue rates) or 'cpu' "
+                         "(CPU baselines of configs 0, 2, 3, 4)")
     ap.add_argument("--offload-steps", type=int, default=512, help="decode steps of the expert-offload leg")
     ap.add_argument("--weight-layout", choices=("tiled", "checkpoint"), default="tiled",
                     help="packed expert weights in HBM: the MFMA-tiled layout (default) or the checkpoint layout")
@@ -392,6 +393,33 @@ def measure_routed_layer(dev, gen, steps=200, n_sets=8):
     return res
 
 
+def measure_mfma_rate(dev, n_wg=2048, iters=20000):
+    """What the matrix cores sustain per scaled-MFMA shape and operand pair (the
+    ceiling the grouped GEMMs are judged against besides the published peaks):
+    one launch of dsv4_probe_mfma_rate per variant, 8 workgroups of 4 waves per CU,
+    timed with events on the launch's stream after an untimed short launch."""
+    import ctypes
+    from dsv4_hip import _lib
+    out = torch.empty(n_wg * 256, dtype=torch.float32, device=dev)
+    st = torch.cuda.current_stream(dev)
+    flop = ctypes.c_double(0.0)
+    res = {}
+    for shape, sname in ((0, "16x16x128"), (1, "32x32x64")):
+        for fa, fb, fname in ((4, 4, "fp4xfp4"), (0, 4, "fp8xfp4"), (0, 0, "fp8xfp8")):
+            _lib.call("dsv4_probe_mfma_rate", shape, fa, fb, n_wg, 16, out.data_ptr(), None, st.cuda_stream)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            _lib.call("dsv4_probe_mfma_rate", shape, fa, fb, n_wg, iters, out.data_ptr(), ctypes.addressof(flop),
+                      st.cuda_stream)
+            e1.record(st)
+            e1.synchronize()
+            s = e0.elapsed_time(e1) * 1e-3
+            peak = MXFP4_PEAK_TFLOPS if fname == "fp4xfp4" else FP8_PEAK_TFLOPS
+            res[f"{sname}_{fname}"] = {"tflops": flop.value / s / 1e12, "frac_published_peak": flop.value / s / 1e12 / peak,
+                                       "ms": s * 1e3}
+    return res
+
+
 def measure_router(dev, iters=200):
     """dsv4_moe_route (gate logits + score + top-8 + weights) at decode and prefill
     token counts: 256 experts, hidden 4096, fp32 gate weight, sqrt(softplus) scores
@@ -624,6 +652,8 @@ def main():
             del host, dev_b
         del pools, tables, runner
         torch.cuda.empty_cache()
+    if not args.no_extra and args.only in ("", "mfma"):
+        extra["mfma_rate"] = measure_mfma_rate(dev)
     if not args.no_extra and args.only in ("", "router"):
         extra["router"] = measure_router(dev)
     if not args.no_extra and args.only in ("", "routed"):

@@ -52,6 +52,17 @@ const char* dsv4_last_error(void) { return g_last_error.c_str(); }
 
 int dsv4_abi_version(void) { return DSV4_ABI_VERSION; }
 
+int dsv4_probe_mfma_rate(int shape, int fmt_a, int fmt_b, int n_wg, int iters, float* out, double* flop,
+                         void* stream) {
+  REQUIRE(shape == 0 || shape == 1, DSV4_ERR_UNSUPPORTED, "mfma probe: shape %d (0: 16x16x128, 1: 32x32x64)", shape);
+  REQUIRE((fmt_a == 4 && fmt_b == 4) || (fmt_a == 0 && fmt_b == 4) || (fmt_a == 0 && fmt_b == 0),
+          DSV4_ERR_UNSUPPORTED, "mfma probe: format pair (%d, %d)", fmt_a, fmt_b);
+  REQUIRE(n_wg > 0 && iters > 0, DSV4_ERR_SHAPE, "mfma probe: n_wg=%d iters=%d", n_wg, iters);
+  REQUIRE(out, DSV4_ERR_NULL, "mfma probe: null output");
+  return hip_status(launch_mfma_rate_probe(shape, fmt_a, fmt_b, n_wg, iters, out, flop, (hipStream_t)stream),
+                    "mfma probe launch");
+}
+
 // ---------------------------------------------------------------------------
 int dsv4_mxfp4_dequant_bf16(const void* packed, const void* scales, void* out, int64_t n_rows, int64_t k,
                             void* stream) {

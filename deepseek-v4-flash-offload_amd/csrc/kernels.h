@@ -130,6 +130,9 @@ hipError_t launch_moe_gemm_down(const Dsv4GemmArgs& a, hipStream_t st);
 // gate/up (with the same epilogue options) or down.
 bool moe_gemm_big_supported(int kdim, int n, bool gateup);
 hipError_t launch_moe_gemm_big(const Dsv4GemmArgs& a, bool gateup, hipStream_t st);
+// MFMA issue-rate probe (probe.hip): shape 0 = 16x16x128, 1 = 32x32x64
+hipError_t launch_mfma_rate_probe(int shape, int fmt_a, int fmt_b, int n_wg, int iters, float* out, double* flop,
+                                  hipStream_t st);
 bool moe_gemm_supported_kdim(int kdim);  // reduction lengths with a compiled kernel (512..4096, powers of two)
 bool moe_gemm_supported_block_m(int bm);  // 16 (decode kernel), 64 or 128 (tiled kernel), 256 (large-tile kernel)
 

@@ -89,6 +89,7 @@ SIGNATURES = {
     "dsv4_slots_invalidate": (_i32, [_c_p, _c_p]),
     "dsv4_slots_stats": (_i32, [_c_p, _c_p]),
     "dsv4_slots_reset_stats": (_i32, [_c_p]),
+    "dsv4_probe_mfma_rate": (_i32, [_i32, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p]),
 }
 
 _LIB = None

@@ -336,6 +336,18 @@ int dsv4_slots_invalidate(dsv4_slots* s, void* compute_stream);
 int dsv4_slots_stats(dsv4_slots* s, int64_t* stats);
 int dsv4_slots_reset_stats(dsv4_slots* s);
 
+/* ---- Measurement helper (no counterpart in the reference) -------------------
+ * One launch of an MFMA issue-rate loop, for the roofline of the grouped GEMMs:
+ * n_wg workgroups of 4 waves, each wave running `iters` iterations of
+ * independent chains of v_mfma_scale_f32_16x16x128_f8f6f4 (shape 0) or
+ * v_mfma_scale_f32_32x32x64_f8f6f4 (shape 1) on register operands (no memory
+ * traffic in the loop). fmt_a / fmt_b: DSV4_AFMT_E4M3 (0) or DSV4_AFMT_E2M1
+ * (4); the pairs E2M1 x E2M1, E4M3 x E2M1 and E4M3 x E4M3. out: n_wg * 256
+ * floats of device memory (one result per thread, so nothing is optimised
+ * away). *flop (nullable): the dense FLOPs the launch performs. */
+int dsv4_probe_mfma_rate(int shape, int fmt_a, int fmt_b, int n_wg, int iters, float* out, double* flop,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif
