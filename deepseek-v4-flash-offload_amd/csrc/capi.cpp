@@ -380,7 +380,14 @@ struct LayerWs {
 // few to fill a launch of their own: measured with Zipf(1.1) routing over 256 experts
 // (hidden 4096, inter 2048), the two-launch split lost 2-10% at 2048-6144 tokens and
 // gained 2% at 8192, 5% at 12288 and 7-10% at 16384.
-constexpr int64_t kHotLayerRows = 65536;
+// DSV4_HOT_LAYER_ROWS overrides it, read once.
+static int64_t hot_layer_rows() {
+  static const int64_t v = [] {
+    const char* s = getenv("DSV4_HOT_LAYER_ROWS");
+    return s ? (int64_t)atoll(s) : (int64_t)65536;
+  }();
+  return v;
+}
 
 static int hot_rows_threshold() {
   static const int v = [] {
@@ -421,7 +428,7 @@ static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool sha
   w.align_scratch = R > kAlignSmallRows ? take(align_chunked_scratch_bytes((int)R, E)) : 0;
   w.route_part = routed ? take(dsv4_moe_route_workspace_bytes(T, D, E)) : -1;  // router partial logits
   const int hot = hot_rows_threshold();
-  if (R >= kHotLayerRows && R > kAlignSmallRows && hot > 0 && moe_gemm_big_supported(D, I, true) &&
+  if (R >= hot_layer_rows() && R > kAlignSmallRows && hot > 0 && moe_gemm_big_supported(D, I, true) &&
       moe_gemm_big_supported(I, D, false)) {
     w.hot_min = hot;
     // each hot expert holds >= hot_min rows: blocks <= R/256 + min(E, R/hot_min) + 1
