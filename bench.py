@@ -237,13 +237,19 @@ def measure_pcie(dev, record_bytes):
     return out
 
 
-def measure_offload(dev, n_steps=512, n_layers=8, n_slots=512, T=8, K=8, warmup_steps=32):
+def measure_offload(dev, n_steps=512, n_layers=8, n_slots=512, T=8, K=8, warmup_steps=32, prefetch_steps=128):
     """Expert offload: every layer's 256 experts in a pinned host pool, ``n_slots`` device
     slots shared by all layers (LRU), decode steps of T tokens with per-layer Zipf routing
     whose hot set drifts. A miss is one record copy on the slot cache's copy stream; the
     compute stream waits for it, so exposed copy time is part of the layer time. Host-side
     work (unique ids, slot acquisition, table upload) is inside the timed region, as it is
-    for a serving loop."""
+    for a serving loop.
+
+    A second timed phase (``prefetch_steps`` more steps on the same cache) prefetches, right
+    after each layer's acquire, the experts the next layer will route to: the copy stream
+    then never waits for a layer's routing to learn its misses. The prefetch is told the
+    next layer's true experts, so this phase bounds what next-layer prefetch can give
+    (a predictor, such as routing with the next layer's gate, would miss some)."""
     from dsv4_hip import ops, synth, PROFILE_BF16, RULE_OCP_FLOOR
     from dsv4_hip.slots import SlotCache, SlotLayout
     base = [{k: torch.from_numpy(v) for k, v in synth.expert_weights(e, D, I).items()} for e in range(8)]
@@ -256,7 +262,7 @@ def measure_offload(dev, n_steps=512, n_layers=8, n_slots=512, T=8, K=8, warmup_
             pinned &= cache.register(l, e, base[(l * 7 + e) % len(base)])
     t_reg = time.perf_counter() - t0
     route = synth.DriftingZipf(n_layers, E, K)
-    total = warmup_steps + n_steps
+    total = warmup_steps + n_steps + prefetch_steps
     ids_all = np.stack([np.stack(route.step(T)) for _ in range(total)])       # [steps, L, T, K]
     w_all = np.stack([synth.routing_weights(T, K, 1000 + s) for s in range(total)])
     ids_dev = torch.from_numpy(ids_all).to(dev)
@@ -266,10 +272,14 @@ def measure_offload(dev, n_steps=512, n_layers=8, n_slots=512, T=8, K=8, warmup_
     runner = ops.LayerRunner(dev, E, D, I)
     ys = [torch.empty((T, D), dtype=torch.bfloat16, device=dev) for _ in range(n_layers)]
 
-    def run(s0, s1):
+    def run(s0, s1, prefetch=False):
         for s in range(s0, s1):
             for l in range(n_layers):
                 slots, _ = cache.acquire(l, uniq[s][l])
+                if prefetch:
+                    ns, nl = (s, l + 1) if l + 1 < n_layers else (s + 1, 0)
+                    if ns < s1:
+                        cache.prefetch(nl, uniq[ns][nl])
                 table = cache.table(uniq[s][l], slots, E)
                 runner.forward(x, ids_dev[s, l], w_dev[s], table, profile=PROFILE_BF16, rule=RULE_OCP_FLOOR,
                                out=ys[l])
@@ -278,7 +288,7 @@ def measure_offload(dev, n_steps=512, n_layers=8, n_slots=512, T=8, K=8, warmup_
     torch.cuda.synchronize()
     cache.reset_stats()
     t0 = time.perf_counter()
-    run(warmup_steps, total)
+    run(warmup_steps, warmup_steps + n_steps)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     st = cache.stats()
@@ -291,6 +301,19 @@ def measure_offload(dev, n_steps=512, n_layers=8, n_slots=512, T=8, K=8, warmup_
            "hit_rate": st["hits"] / max(lookups, 1), "misses_per_step": st["misses"] / n_steps,
            "h2d_gb": st["bytes_h2d"] / 1e9, "h2d_effective_gbs": st["bytes_h2d"] / wall / 1e9,
            "evictions": st["evictions"]}
+    if prefetch_steps > 0:
+        cache.reset_stats()
+        t0 = time.perf_counter()
+        run(warmup_steps + n_steps, total, prefetch=True)
+        torch.cuda.synchronize()
+        wall_pf = time.perf_counter() - t0
+        sp = cache.stats()
+        lp = sp["hits"] + sp["misses"]
+        res["prefetch_next_upper_bound"] = {
+            "steps": prefetch_steps, "ms_per_layer": wall_pf / (prefetch_steps * n_layers) * 1e3,
+            "hit_rate": sp["hits"] / max(lp, 1), "misses_per_step": sp["misses"] / prefetch_steps,
+            "prefetched_per_step": sp["prefetched"] / prefetch_steps,
+            "h2d_effective_gbs": sp["bytes_h2d"] / wall_pf / 1e9}
     res.update(measure_pcie(dev, layout.record_bytes))
     cache.close()
     del cache, ys, runner
