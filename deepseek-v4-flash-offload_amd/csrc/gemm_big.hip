@@ -55,7 +55,6 @@ constexpr int kBN = 256;     // weight rows per block
 constexpr int kNT = 256;     // threads (4 waves, one per SIMD)
 constexpr int kKS = 64;      // k per stage
 constexpr int kSS = 16;      // stages per scale super-stage (1024 k)
-constexpr int kSPitch = 40;  // scale row pitch: the 32 rows of a byte read land on distinct banks
 
 template <int AFMT>
 struct Big {
@@ -66,12 +65,14 @@ struct Big {
   static constexpr int AV = ACH / 4;                  // A loads per thread per stage
   static constexpr int BV = BCH / 4;                  // weight loads per thread per stage
   static constexpr int L = AV + BV;
-  // scales: one super-stage = 32 bytes per A row and per weight row, brought in by
-  // two 16-byte loads per row into registers once per 16 stages (the L2 requests,
-  // not the bytes, are what costs), double-buffered in LDS
-  static constexpr int SCL = 2 * kBM * kSPitch;
+  // scales: one super-stage = 32 bytes per A row and per weight row (two 16-byte
+  // pieces), loaded by LDS-DMA once per 16 stages into one of two buffers; a buffer
+  // holds the A rows' then the weight rows' pieces, each half-major:
+  // [half][row] x 16 bytes
+  static constexpr int SCL = 2 * (kBM + kBN) * 16;
   static constexpr int AS_OFF = NB * STAGE;
-  static constexpr int BS_OFF = AS_OFF + kBM * kSPitch;
+  static constexpr int BS_OFF = kBM * 32;            // weight rows within a buffer
+  static constexpr int SV = SCL / (kNT * 16);         // scale loads per thread per super-stage
   static constexpr int LDS = NB * STAGE + 2 * SCL;
   static_assert(LDS <= 160 * 1024, "the stage ring and two scale super-stages must fit the LDS");
   static_assert(BCH == 8 && (ACH * 1024) == kBM * (AFMT == 0 ? kKS : kKS / 2), "chunking");
@@ -106,32 +107,20 @@ DSV4_DEV void wait_loads_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// one super-stage of scales for thread tid: A row tid's 32 bytes, weight row tid's 32 bytes
-struct BigScales {
-  v4i a[2], b[2];
-};
-
-DSV4_DEV void big_load_scales(BigScales& sc, const uint8_t* sa_src, const uint8_t* sb_src, int ss) {
-  sc.a[0] = *(gv4i*)(sa_src + ss * 32);
-  sc.a[1] = *(gv4i*)(sa_src + ss * 32 + 16);
-  sc.b[0] = *(gv4i*)(sb_src + ss * 32);
-  sc.b[1] = *(gv4i*)(sb_src + ss * 32 + 16);
+// Issues the scale loads of super-stage ss into buffer `buf` (sc_src: this lane's
+// pieces at super-stage 0, in load order (wave * SV + v) * 64 + lane).
+template <int AFMT>
+DSV4_DEV void big_dma_scales(uint8_t* lds, int buf, const uint8_t* const* sc_src, int wave, int ss) {
+  using C = Big<AFMT>;
+#pragma unroll
+  for (int v = 0; v < C::SV; ++v) dma16(sc_src[v] + ss * 32, lds + C::AS_OFF + buf * C::SCL + (wave * C::SV + v) * 1024);
 }
 
-template <int AFMT>
-DSV4_DEV void big_store_scales(const BigScales& sc, uint8_t* lds, int buf, int tid) {
-  using C = Big<AFMT>;
-  typedef int v2i __attribute__((ext_vector_type(2)));
-  uint8_t* pa = lds + C::AS_OFF + buf * C::SCL + tid * kSPitch;
-  uint8_t* pb = lds + C::BS_OFF + buf * C::SCL + tid * kSPitch;
-  *(v2i*)(pa + 0) = v2i{sc.a[0].x, sc.a[0].y};
-  *(v2i*)(pa + 8) = v2i{sc.a[0].z, sc.a[0].w};
-  *(v2i*)(pa + 16) = v2i{sc.a[1].x, sc.a[1].y};
-  *(v2i*)(pa + 24) = v2i{sc.a[1].z, sc.a[1].w};
-  *(v2i*)(pb + 0) = v2i{sc.b[0].x, sc.b[0].y};
-  *(v2i*)(pb + 8) = v2i{sc.b[0].z, sc.b[0].w};
-  *(v2i*)(pb + 16) = v2i{sc.b[1].x, sc.b[1].y};
-  *(v2i*)(pb + 24) = v2i{sc.b[1].z, sc.b[1].w};
+// The E8M0 byte q (0..31, the 32-k block within the super-stage) of row `row` of the
+// A (B = false) or weight (B = true) rows in scale buffer S.
+template <bool B>
+DSV4_DEV int scale_byte(const uint8_t* S, int row, int q) {
+  return S[(B ? kBM * 32 : 0) + ((q >> 4) * (B ? kBN : kBM) + row) * 16 + (q & 15)];
 }
 
 // Issues stage s's loads into ring slot `slot`: this wave's A chunks wave * AV + v and
@@ -170,7 +159,7 @@ DSV4_DEV void big_read(BigFrag<AFMT>& F, const uint8_t* L, const uint8_t* S, int
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt) {
     F.b[nt] = *(const v4i*)(L + (C::ACH + brow0[nt] / 32) * 1024 + b_lane);
-    F.sb[nt] = S[kBM * kSPitch + (brow0[nt] + r32) * kSPitch + q0 + g2];
+    F.sb[nt] = scale_byte<true>(S, brow0[nt] + r32, q0 + g2);
   }
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
@@ -182,7 +171,7 @@ DSV4_DEV void big_read(BigFrag<AFMT>& F, const uint8_t* L, const uint8_t* S, int
     } else {
       F.lo[mt] = *(const v4i*)(L + (row0 / 32) * 1024 + a_lo);
     }
-    F.sa[mt] = S[(row0 + r32) * kSPitch + q0 + g2];
+    F.sa[mt] = scale_byte<false>(S, row0 + r32, q0 + g2);
   }
 }
 
@@ -339,14 +328,21 @@ __global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
     b_src[v] = w + (tiled ? (int64_t)((gtile * (p.Kdim / 256)) * 2 + ji) * 1024 + 16 * r
                           : (int64_t)(16 * gtile + r) * wrow_bytes + 16 * ji);
   }
-  const uint8_t* sa_src;
-  const uint8_t* sb_src;
-  {
-    const int f = p.sorted_ids[slot0 + tid];
-    const int arow = f < p.R ? f / p.a_row_div : 0;
-    sa_src = p.a_scale + (int64_t)arow * srow;
-    const uint8_t* ws = GATEUP ? (tid < 128 ? ex.w1s : ex.w3s) : ex.w2s;
-    sb_src = ws + (int64_t)(GATEUP ? c0 + (tid & 127) : c0 + tid) * srow;
+  // this lane's scale pieces (super-stage 0): piece q = (wave * SV + v) * 64 + lane of a
+  // buffer: A rows for q < 512, weight rows after; half (q / 256) % 2, row q % 256
+  const uint8_t* sc_src[C::SV];
+#pragma unroll
+  for (int v = 0; v < C::SV; ++v) {
+    const int q = (wave * C::SV + v) * 64 + lane;
+    const int half = (q >> 8) & 1, row = q & 255;
+    if (q < 2 * kBM) {
+      const int f = p.sorted_ids[slot0 + row];
+      const int arow = f < p.R ? f / p.a_row_div : 0;
+      sc_src[v] = p.a_scale + (int64_t)arow * srow + 16 * half;
+    } else {
+      const uint8_t* ws = GATEUP ? (row < 128 ? ex.w1s : ex.w3s) : ex.w2s;
+      sc_src[v] = ws + (int64_t)(GATEUP ? c0 + (row & 127) : c0 + row) * srow + 16 * half;
+    }
   }
 
   v16f acc[4][4];
@@ -388,16 +384,17 @@ __global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
     // the compiler move the MFMAs away from their stage): past the last stage the loads
     // repeat stage NST - 1 into slots that are never read again, so every stage issues
     // the same number of loads and the wait count stays exact. Scales: super-stage ss
-    // (stages 16ss..16ss+15) in LDS buffer ss % 2, written between stages 16ss - 1 and
-    // 16ss from registers loaded 16 stages earlier (past the end: a repeat of the last
-    // one into the buffer no stage reads). NST = K / 64 is a multiple of 16.
+    // (stages 16ss..16ss+15) in LDS buffer ss % 2, loaded by LDS-DMA between stages
+    // 16ss - 17 and 16ss - 16, once the buffer's previous super-stage has been read
+    // (past the end: a repeat of the last one into the buffer no stage reads); those
+    // loads are younger than the stage loads the next waits count, so the waits only
+    // grow stricter. Scales in registers would make the compiler drain every load in
+    // flight before storing them (it cannot see that 16 stages have passed). NST =
+    // K / 64 is a multiple of 16.
     const int NSS = NST / kSS;
-    BigScales sc;
-    big_load_scales(sc, sa_src, sb_src, 0);
+    big_dma_scales<AFMT>(lds, 0, sc_src, wave, 0);
 #pragma unroll
     for (int t = 0; t < C::NB; ++t) big_dma_stage<AFMT>(lds + t * C::STAGE, a_src, b_src, wave, bj, bg, t);
-    big_store_scales<AFMT>(sc, lds, 0, tid);
-    big_load_scales(sc, sa_src, sb_src, min(1, NSS - 1));
     wait_loads_barrier<C::L * (C::NB - 1)>();
     BigFrag<AFMT> f0, f1;
     big_read<AFMT>(f0, lds, lds + C::AS_OFF, 0, wm, brow0, r32, g2, a_lo, a_hi, b_lane);
@@ -417,8 +414,7 @@ __global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
   }
 #pragma unroll 1
     for (int ss = 0; ss < NSS; ++ss) {
-      big_store_scales<AFMT>(sc, lds, (ss + 1) & 1, tid);
-      big_load_scales(sc, sa_src, sb_src, min(ss + 2, NSS - 1));
+      big_dma_scales<AFMT>(lds, (ss + 1) & 1, sc_src, wave, min(ss + 1, NSS - 1));
 #pragma unroll 1
       for (int s = kSS * ss; s < kSS * (ss + 1); ++s) {
         DSV4_BIG_STEP(f0, f1);
