@@ -122,9 +122,29 @@ def lib():
     return _LIB
 
 
+_FN = {}
+_RAW_STREAM = None
+
+
+def stream_handle(device):
+    """torch's current stream on ``device`` as the raw handle the entry points take
+    (read without building a torch Stream object per call)."""
+    global _RAW_STREAM
+    import torch
+    if _RAW_STREAM is None:
+        _RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", False)
+    if _RAW_STREAM:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _RAW_STREAM(idx)
+    return torch.cuda.current_stream(device).cuda_stream
+
+
 def call(name, *args):
     """Call a status-returning entry point and raise ``Dsv4Error`` on failure."""
-    rc = getattr(lib(), name)(*args)
+    fn = _FN.get(name)
+    if fn is None:
+        fn = _FN[name] = getattr(lib(), name)
+    rc = fn(*args)
     if rc != DSV4_OK:
         msg = lib().dsv4_last_error().decode(errors="replace")
         raise Dsv4Error(name, rc, msg)

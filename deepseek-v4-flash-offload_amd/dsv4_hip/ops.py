@@ -12,7 +12,7 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import call
+from ._lib import call, stream_handle
 
 _E8M0 = getattr(torch, "float8_e8m0fnu", None)
 
@@ -27,17 +27,20 @@ def _dev(t: torch.Tensor, what: str) -> torch.Tensor:
 
 
 def _u8(t: torch.Tensor) -> torch.Tensor:
+    if t.dtype == torch.uint8 and t.is_contiguous():
+        return t
     if t.dtype in (torch.uint8, torch.int8) or (_E8M0 is not None and t.dtype == _E8M0):
         return t.contiguous().view(torch.uint8)
     raise TypeError(f"expected a byte tensor (uint8/int8/e8m0), got {t.dtype}")
 
 
 def _p(t: Optional[torch.Tensor]):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    # the bound entry points declare pointer arguments c_void_p, which takes the int as is
+    return None if t is None else t.data_ptr()
 
 
 def _stream(t: torch.Tensor):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    return stream_handle(t.device)
 
 
 # ---------------------------------------------------------------------------

@@ -16,7 +16,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from ._lib import call
+from ._lib import call, stream_handle
 
 FIELDS = ("w1p", "w1s", "w2p", "w2s", "w3p", "w3s")
 PACKED = ("w1p", "w2p", "w3p")
@@ -115,7 +115,7 @@ class SlotCache:
 
     # -- device slots ------------------------------------------------------
     def _stream(self):
-        return ctypes.c_void_p(torch.cuda.current_stream(self.device).cuda_stream)
+        return stream_handle(self.device)
 
     def acquire(self, layer, eids):
         """Makes experts resident; returns (slots int32 array, n_miss)."""

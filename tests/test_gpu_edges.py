@@ -9,7 +9,7 @@ import torch
 
 from oracle import moe as M
 from oracle import mxfp4 as Q
-from dsv4_hip import ops, synth, PROFILE_A4W4, PROFILE_BF16, RULE_OCP_FLOOR
+from dsv4_hip import ops, synth, AFMT_E2M1, AFMT_E4M3, PROFILE_A4W4, PROFILE_BF16, RULE_OCP_FLOOR
 
 pytestmark = pytest.mark.gpu
 
@@ -104,3 +104,47 @@ def test_out_of_range_ids_add_nothing(gpu, n_rows_T):
     al = ops.moe_align(torch.from_numpy(bad).to(gpu), torch.from_numpy(w).to(gpu), E, 16)
     torch.cuda.synchronize()
     assert int(al.status.item()) == 2
+
+
+@pytest.mark.parametrize("bm", [16, 64, 128, 256])
+@pytest.mark.parametrize("profile", ["bf16", "a4w4"])
+def test_missing_experts_gemm_rows(gpu, profile, bm):
+    # every kernel (16-row, 64/128-row tiled, 256-row large-tile) on a table with three
+    # routed experts empty, among them the one with the most rows: their rows of h and
+    # of the down output are exactly zero, every other row bit for bit what the full
+    # table gives
+    T, K, E, D, I = 300, 6, 24, 2048, 1024
+    ids = synth.zipf_topk(T, K, E, synth.rank_permutation(E, 3), np.random.default_rng(21))
+    w = synth.routing_weights(T, K, 22)
+    x = synth.bf16_normal(np.random.default_rng(23), (T, D)).to(gpu)
+    counts = np.bincount(ids.reshape(-1), minlength=E)
+    used = np.unique(ids)
+    missing = {int(np.argmax(counts)), int(used[0]), int(used[-1])}
+    devw = {int(e): {k: torch.from_numpy(v).to(gpu) for k, v in synth.expert_weights(int(e), D, I).items()}
+            for e in used}
+    full = ops.expert_table(devw, E, gpu)
+    part = ops.expert_table({e: d for e, d in devw.items() if e not in missing}, E, gpu)
+    al = ops.moe_align(torch.from_numpy(ids).to(gpu), torch.from_numpy(w).to(gpu), E, bm)
+    wf = torch.from_numpy(w.reshape(-1)).to(gpu)
+    if profile == "bf16":
+        q = ops.fp8_act_quant(x, 128, want_codes=True, want_e8m0x4=True)
+        a, a_s, afmt = q["codes"], q["e8m0x4"], AFMT_E4M3
+    else:
+        a, a_s, _ = ops.mxfp4_act_quant(x, RULE_OCP_FLOOR)
+        afmt = AFMT_E2M1
+    h_full = ops.gemm_gateup(afmt, a, a_s, K, al, full, D, I, wf, 10.0)
+    h_part = ops.gemm_gateup(afmt, a, a_s, K, al, part, D, I, wf, 10.0)
+    if profile == "bf16":
+        q = ops.fp8_act_quant(h_full, 128, want_codes=True, want_e8m0x4=True)
+        ha, has = q["codes"], q["e8m0x4"]
+    else:
+        ha, has, _ = ops.mxfp4_act_quant(h_full, RULE_OCP_FLOOR)
+    o_full = ops.gemm_down(afmt, ha, has, al, full, I, D)
+    o_part = ops.gemm_down(afmt, ha, has, al, part, I, D)
+    torch.cuda.synchronize()
+    gone = torch.from_numpy(np.isin(ids.reshape(-1), list(missing))).to(gpu)
+    print(f"{profile} bm={bm}: {int(gone.sum())} of {T * K} rows on missing experts {sorted(missing)}")
+    for name, got, ref in (("h", h_part, h_full), ("down", o_part, o_full)):
+        assert float(got[gone].float().abs().max()) == 0.0, f"{name}: rows of missing experts are not zero"
+        assert torch.equal(got.view(torch.int16)[~gone], ref.view(torch.int16)[~gone]), \
+            f"{name}: rows of present experts differ"
