@@ -43,7 +43,11 @@ constexpr int kRouteWaves = 4;  // waves per workgroup in both kernels
 // = hi, mid, lo): every product is exact in fp32 and the accumulation is fp32,
 // at about five times the fp32 MFMA's rate. Lane (r, g) feeds the same 8 k's
 // to A and B, so the hardware's pairing of A and B elements is all that matters.
-template <bool XF32, int MT, int NT, bool BF3 = false>
+//
+// NSTEP > 0: the chunk is exactly NSTEP steps and every one of its loads is issued
+// before the first MFMA (decode-sized T: a few hundred waves each stream 16 expert
+// rows, and a step-by-step prefetch would pay one memory latency per step).
+template <bool XF32, int MT, int NT, bool BF3 = false, int NSTEP = 0>
 __global__ __launch_bounds__(64 * kRouteWaves) void route_logits_kernel(const void* __restrict__ xp,
                                                                          const float* __restrict__ w, int T,
                                                                          int D, int E, int kchunk,
@@ -64,11 +68,11 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_logits_kernel(const vo
   }
 #pragma unroll
   for (int n = 0; n < NT; ++n) wr[n] = w + (int64_t)min(e0 + 16 * n + r, E - 1) * D + k0;
-  // 8 x values of token row m at k offset kb: two uint4 of fp32, or one uint4 of bf16
+  // 8 x values of token row m at k offset kb: two uint4 of fp32, or one uint4 of bf16.
+  // Rows past T read row 0 (no branch around the load): a token row of the product
+  // depends on its own x row only, and those rows are never stored.
   auto load_x = [&](int m, int kb, uint4& a, uint4& b) {
-    if (!live[m]) {
-      a = b = make_uint4(0u, 0u, 0u, 0u);
-    } else if (XF32) {
+    if (XF32) {
       const uint4* p = (const uint4*)((const float*)xp + xoff[m] + kb);
       a = p[0];
       b = p[1];
@@ -82,20 +86,12 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_logits_kernel(const vo
   for (int m = 0; m < MT; ++m)
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc[m][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // one step of loads in flight while the previous step's MFMAs run
-  uint4 xa[MT], xb[MT];
-  float4 wa[NT], wb[NT];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) load_x(m, 0, xa[m], xb[m]);
-#pragma unroll
-  for (int n = 0; n < NT; ++n) wa[n] = *(const float4*)wr[n], wb[n] = *(const float4*)(wr[n] + 4);
-  for (int kb = 0; kb < kchunk; kb += 32) {
+  // the MFMAs of one step on its loaded x (xa, xb) and weights (wa, wb)
+  auto step = [&](const uint4 (&xa)[MT], const uint4 (&xb)[MT], const float4 (&wa)[NT], const float4 (&wb)[NT]) {
     float xf[MT][8], wf[NT][8];
-    uint4 xa_cur[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
       const uint4 u = xa[m], v = xb[m];
-      xa_cur[m] = u;
       if (XF32) {
         xf[m][0] = __uint_as_float(u.x), xf[m][1] = __uint_as_float(u.y);
         xf[m][2] = __uint_as_float(u.z), xf[m][3] = __uint_as_float(u.w);
@@ -112,13 +108,6 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_logits_kernel(const vo
     for (int n = 0; n < NT; ++n) {
       wf[n][0] = wa[n].x, wf[n][1] = wa[n].y, wf[n][2] = wa[n].z, wf[n][3] = wa[n].w;
       wf[n][4] = wb[n].x, wf[n][5] = wb[n].y, wf[n][6] = wb[n].z, wf[n][7] = wb[n].w;
-    }
-    if (kb + 32 < kchunk) {
-#pragma unroll
-      for (int m = 0; m < MT; ++m) load_x(m, kb + 32, xa[m], xb[m]);
-#pragma unroll
-      for (int n = 0; n < NT; ++n)
-        wa[n] = *(const float4*)(wr[n] + kb + 32), wb[n] = *(const float4*)(wr[n] + kb + 36);
     }
     if constexpr (BF3) {
 #pragma unroll
@@ -147,7 +136,7 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_logits_kernel(const vo
         const bf16x8 bl = __builtin_bit_cast(bf16x8, make_uint4(lo[0], lo[1], lo[2], lo[3]));
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-          const bf16x8 a = __builtin_bit_cast(bf16x8, xa_cur[m]);
+          const bf16x8 a = __builtin_bit_cast(bf16x8, xa[m]);
           acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bl, acc[m][n], 0, 0, 0);
           acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bm, acc[m][n], 0, 0, 0);
           acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bh, acc[m][n], 0, 0, 0);
@@ -161,6 +150,46 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_logits_kernel(const vo
 #pragma unroll
           for (int n = 0; n < NT; ++n)
             acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[m][i], wf[n][i], acc[m][n], 0, 0, 0);
+    }
+  };
+  if constexpr (NSTEP > 0) {
+    // the whole chunk's loads, then its MFMAs
+    uint4 xa[NSTEP][MT], xb[NSTEP][MT];
+    float4 wa[NSTEP][NT], wb[NSTEP][NT];
+#pragma unroll
+    for (int q = 0; q < NSTEP; ++q) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m) load_x(m, 32 * q, xa[q][m], xb[q][m]);
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+        wa[q][n] = *(const float4*)(wr[n] + 32 * q), wb[q][n] = *(const float4*)(wr[n] + 32 * q + 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // (else the scheduler sinks each load to its use)
+#pragma unroll
+    for (int q = 0; q < NSTEP; ++q) step(xa[q], xb[q], wa[q], wb[q]);
+  } else {
+    // one step of loads in flight while the previous step's MFMAs run
+    uint4 xa[MT], xb[MT];
+    float4 wa[NT], wb[NT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) load_x(m, 0, xa[m], xb[m]);
+#pragma unroll
+    for (int n = 0; n < NT; ++n) wa[n] = *(const float4*)wr[n], wb[n] = *(const float4*)(wr[n] + 4);
+    for (int kb = 0; kb < kchunk; kb += 32) {
+      uint4 ca[MT], cb[MT];
+      float4 cwa[NT], cwb[NT];
+#pragma unroll
+      for (int m = 0; m < MT; ++m) ca[m] = xa[m], cb[m] = xb[m];
+#pragma unroll
+      for (int n = 0; n < NT; ++n) cwa[n] = wa[n], cwb[n] = wb[n];
+      if (kb + 32 < kchunk) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) load_x(m, kb + 32, xa[m], xb[m]);
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+          wa[n] = *(const float4*)(wr[n] + kb + 32), wb[n] = *(const float4*)(wr[n] + kb + 36);
+      }
+      step(ca, cb, cwa, cwb);
     }
   }
   // C lane l holds C[4(l/16) + i][l%16]: token t0 + 16m + 4g + i, expert e0 + 16n + r.
@@ -199,9 +228,15 @@ struct RouteTile {
 };
 static RouteTile route_tile(int T) { return T >= 256 ? RouteTile{4, 2} : RouteTile{1, 1}; }
 
+// The decode-sized tile streams chunks of exactly this many k, every load issued up
+// front (route_logits_kernel's NSTEP = kRouteSmallChunk / 32).
+constexpr int kRouteSmallChunk = 256;
+static bool route_small_chunks(int T, int D) { return route_tile(T).mt == 1 && D % kRouteSmallChunk == 0; }
+
 // K split so that about 2048 waves (two per SIMD) run, with chunks of at least
-// 256 k that stay multiples of 32.
+// 256 k that stay multiples of 32; decode-sized T: chunks of exactly 256 k.
 int route_split_k(int T, int D, int E) {
+  if (route_small_chunks(T, D)) return D / kRouteSmallChunk;
   const RouteTile rt = route_tile(T);
   const int tt = 16 * rt.mt, te = 16 * rt.nt;
   const int tiles = ((E + te - 1) / te) * ((T + tt - 1) / tt);
@@ -223,6 +258,14 @@ hipError_t launch_route_logits(const void* x, int x_f32, const float* gate_w, in
       hipLaunchKernelGGL((route_logits_kernel<true, 4, 2>), g1, b1, 0, st, x, gate_w, T, D, E, D / S, part);
     else
       hipLaunchKernelGGL((route_logits_kernel<false, 4, 2, true>), g1, b1, 0, st, x, gate_w, T, D, E, D / S,
+                         part);
+  } else if (route_small_chunks(T, D)) {
+    constexpr int NS = kRouteSmallChunk / 32;
+    if (x_f32)
+      hipLaunchKernelGGL((route_logits_kernel<true, 1, 1, false, NS>), g1, b1, 0, st, x, gate_w, T, D, E, D / S,
+                         part);
+    else
+      hipLaunchKernelGGL((route_logits_kernel<false, 1, 1, false, NS>), g1, b1, 0, st, x, gate_w, T, D, E, D / S,
                          part);
   } else {
     if (x_f32)

@@ -75,9 +75,15 @@ DSV4_DEV void route_topk_token(const RouteTopkArgs& a, int t, int lane) {
   // the bias and the token's input id are loaded with the partials (one memory
   // latency, not two or three)
   int64_t tok = tid2eid ? load_index(input_ids, ids_is64, t) : -1;
+  // Loads read clamped indices (expert E - 1, chunk S - 1) and the values are dropped
+  // afterwards, so no load sits behind a branch: each would be its own round trip.
   float bv[EPL];
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) bv[j] = (bias && lane + 64 * j < E) ? bias[lane + 64 * j] : 0.f;
+  for (int j = 0; j < EPL; ++j) {
+    const int e = lane + 64 * j;
+    bv[j] = bias ? bias[min(e, E - 1)] : 0.f;
+    if (e >= E) bv[j] = 0.f;
+  }
   float sc[EPL];
   // the S partials of each expert, summed in chunk order; up to 16 chunks' loads in flight
 #pragma unroll
@@ -87,16 +93,17 @@ DSV4_DEV void route_topk_token(const RouteTopkArgs& a, int t, int lane) {
 #pragma unroll
     for (int i = 0; i < 16; ++i)
 #pragma unroll
-      for (int j = 0; j < EPL; ++j) {
-        const int e = lane + 64 * j;
-        v[i][j] = (z0 + i < S && e < E) ? part[((int64_t)(z0 + i) * T + t) * E + e] : 0.f;
-      }
+      for (int j = 0; j < EPL; ++j)
+        v[i][j] = part[((int64_t)min(z0 + i, S - 1) * T + t) * E + min(lane + 64 * j, E - 1)];
 #pragma unroll
     for (int i = 0; i < 16; ++i)
 #pragma unroll
       for (int j = 0; j < EPL; ++j)
         if (z0 + i < S) sc[j] += v[i][j];
   }
+#pragma unroll
+  for (int j = 0; j < EPL; ++j)
+    if (lane + 64 * j >= E) sc[j] = 0.f;
   if (scoring == 0) {  // softmax over the E experts
     float m = ninf;
 #pragma unroll
