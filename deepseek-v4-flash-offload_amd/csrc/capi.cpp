@@ -301,19 +301,28 @@ int dsv4_moe_route(const void* x, int x_f32, const float* gate_w, const float* b
 }
 
 // ---------------------------------------------------------------------------
+static_assert(DSV4_AFMT_BF16 == kAfmtBf16, "A format ids");
+
 static int check_gemm_common(int afmt, const void* a, const void* a_scale, const int32_t* sorted_ids,
-                             const int32_t* block_expert, const int32_t* npp, int R, int max_blocks,
+                             const int32_t* block_expert, const int32_t* npp, int R, int block_m, int max_blocks,
                              const void* experts, int Kdim, void* out) {
-  REQUIRE(afmt == DSV4_AFMT_E4M3 || afmt == DSV4_AFMT_E2M1, DSV4_ERR_UNSUPPORTED, "gemm: unknown A format %d",
-          afmt);
+  REQUIRE(afmt == DSV4_AFMT_E4M3 || afmt == DSV4_AFMT_E2M1 || afmt == DSV4_AFMT_BF16, DSV4_ERR_UNSUPPORTED,
+          "gemm: unknown A format %d", afmt);
+  REQUIRE(afmt != DSV4_AFMT_BF16 || block_m == DSV4_GEMM_BLOCK_M, DSV4_ERR_UNSUPPORTED,
+          "gemm: bf16 activations need block_m %d (got %d)", DSV4_GEMM_BLOCK_M, block_m);
   REQUIRE(R >= 0 && max_blocks >= 0, DSV4_ERR_SHAPE, "gemm: negative size");
   REQUIRE(moe_gemm_supported_kdim(Kdim), DSV4_ERR_UNSUPPORTED,
           "gemm: reduction dim %d unsupported (512, 1024, 2048 or 4096)", Kdim);
-  REQUIRE(a && a_scale && sorted_ids && block_expert && npp && experts && out, DSV4_ERR_NULL,
-          "gemm: null pointer");
+  REQUIRE(a && (a_scale || afmt == DSV4_AFMT_BF16) && sorted_ids && block_expert && npp && experts && out,
+          DSV4_ERR_NULL, "gemm: null pointer");
   REQUIRE(aligned(a, 16) && aligned(a_scale, 4) && aligned(experts, 8), DSV4_ERR_SHAPE,
           "gemm: misaligned buffer");
   return DSV4_OK;
+}
+
+// bytes per A row of a reduction of length k
+static int64_t a_row_bytes(int afmt, int k) {
+  return afmt == DSV4_AFMT_E4M3 ? (int64_t)k : afmt == DSV4_AFMT_E2M1 ? (int64_t)k / 2 : 2 * (int64_t)k;
 }
 
 int dsv4_moe_gemm_gateup(int afmt, const void* a, const void* a_scale, int a_row_div, const int32_t* sorted_ids,
@@ -325,13 +334,13 @@ int dsv4_moe_gemm_gateup(int afmt, const void* a, const void* a_scale, int a_row
   REQUIRE(I > 0 && I % 128 == 0, DSV4_ERR_UNSUPPORTED, "gemm gate/up: I=%d not a multiple of 128", I);
   REQUIRE(a_row_div > 0, DSV4_ERR_SHAPE, "gemm gate/up: a_row_div=%d", a_row_div);
   if (R == 0 || max_blocks == 0) return DSV4_OK;
-  int rc = check_gemm_common(afmt, a, a_scale, sorted_ids, block_expert, num_post_padded, R, max_blocks,
+  int rc = check_gemm_common(afmt, a, a_scale, sorted_ids, block_expert, num_post_padded, R, block_m, max_blocks,
                              expert_table, D, h_out);
   if (rc) return rc;
   REQUIRE(topk_w, DSV4_ERR_NULL, "gemm gate/up: null routing weights");
   REQUIRE(block_m != 256 || moe_gemm_big_supported(D, I, true), DSV4_ERR_UNSUPPORTED,
           "gemm gate/up: 256-row blocks need D a multiple of 1024 and I of 128 (D=%d, I=%d)", D, I);
-  Dsv4GemmArgs g{afmt, (const uint8_t*)a, afmt == DSV4_AFMT_E4M3 ? (int64_t)D : (int64_t)D / 2,
+  Dsv4GemmArgs g{afmt, (const uint8_t*)a, a_row_bytes(afmt, D),
                  (const uint8_t*)a_scale, a_row_div, sorted_ids, block_expert, num_post_padded, R, block_m,
                  max_blocks, (const Dsv4ExpertPtrs*)expert_table, D, I, topk_w, swiglu_limit,
                  (uint16_t*)h_out};
@@ -345,12 +354,12 @@ int dsv4_moe_gemm_down(int afmt, const void* a, const void* a_scale, const int32
           "gemm: block_m %d unsupported (16, 64, 128 or 256)", block_m);
   REQUIRE(D > 0 && D % 256 == 0, DSV4_ERR_UNSUPPORTED, "gemm down: D=%d not a multiple of 256", D);
   if (R == 0 || max_blocks == 0) return DSV4_OK;
-  int rc = check_gemm_common(afmt, a, a_scale, sorted_ids, block_expert, num_post_padded, R, max_blocks,
+  int rc = check_gemm_common(afmt, a, a_scale, sorted_ids, block_expert, num_post_padded, R, block_m, max_blocks,
                              expert_table, I, out);
   if (rc) return rc;
   REQUIRE(block_m != 256 || (moe_gemm_big_supported(I, D, false) && aligned(out, 16)), DSV4_ERR_UNSUPPORTED,
           "gemm down: 256-row blocks need I a multiple of 1024, D of 256 and a 16-byte aligned output");
-  Dsv4GemmArgs g{afmt, (const uint8_t*)a, afmt == DSV4_AFMT_E4M3 ? (int64_t)I : (int64_t)I / 2,
+  Dsv4GemmArgs g{afmt, (const uint8_t*)a, a_row_bytes(afmt, I),
                  (const uint8_t*)a_scale, 1, sorted_ids, block_expert, num_post_padded, R, block_m, max_blocks,
                  (const Dsv4ExpertPtrs*)expert_table, I, D, nullptr, 0.0f, (uint16_t*)out};
   return hip_status(launch_moe_gemm_down(g, (hipStream_t)stream), "gemm down launch");
@@ -407,7 +416,8 @@ static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool sha
   LayerWs w{};
   const int64_t R = (int64_t)T * K;
   const int64_t Rt = R + (shared ? T : 0);  // routed rows, then the shared expert's T rows
-  const int bm = layer_block_m(R);
+  const bool pure = profile == DSV4_PROFILE_BF16_PURE;  // bf16 x and h, the 16-row kernel only
+  const int bm = pure ? DSV4_GEMM_BLOCK_M : layer_block_m(R);
   w.bm = bm;
   w.max_blocks = dsv4_moe_align_max_blocks((int)R, E, bm) + (shared ? (T + bm - 1) / bm : 0);
   const bool fp8 = profile == DSV4_PROFILE_BF16;
@@ -417,18 +427,19 @@ static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool sha
   w.block_expert = take(sizeof(int32_t) * (int64_t)w.max_blocks);
   w.npp = take(sizeof(int32_t));
   w.status = take(sizeof(int32_t));
-  w.xa = take(fp8 ? (int64_t)T * D : (int64_t)T * D / 2);
-  w.xs = take((int64_t)T * D / 32);
+  w.xa = pure ? -1 : take(fp8 ? (int64_t)T * D : (int64_t)T * D / 2);
+  w.xs = pure ? -1 : take((int64_t)T * D / 32);
   // bf16 h only where the gate/up cannot quantise it in its epilogue (FP8
   // blocks of 128 columns span four single-wave workgroups of the 16-row kernel)
-  w.h = (fp8 && bm == DSV4_GEMM_BLOCK_M) ? take(2 * Rt * I) : -1;
-  w.ha = take(fp8 ? Rt * I : Rt * I / 2);
-  w.hs = take(Rt * I / 32);
+  // and for the pure-bf16 variant, whose down GEMM reads it as it is
+  w.h = ((fp8 && bm == DSV4_GEMM_BLOCK_M) || pure) ? take(2 * Rt * I) : -1;
+  w.ha = pure ? -1 : take(fp8 ? Rt * I : Rt * I / 2);
+  w.hs = pure ? -1 : take(Rt * I / 32);
   w.out = take(2 * Rt * D);
   w.align_scratch = R > kAlignSmallRows ? take(align_chunked_scratch_bytes((int)R, E)) : 0;
   w.route_part = routed ? take(dsv4_moe_route_workspace_bytes(T, D, E)) : -1;  // router partial logits
   const int hot = hot_rows_threshold();
-  if (R >= hot_layer_rows() && R > kAlignSmallRows && hot > 0 && moe_gemm_big_supported(D, I, true) &&
+  if (!pure && R >= hot_layer_rows() && R > kAlignSmallRows && hot > 0 && moe_gemm_big_supported(D, I, true) &&
       moe_gemm_big_supported(I, D, false)) {
     w.hot_min = hot;
     // each hot expert holds >= hot_min rows: blocks <= R/256 + min(E, R/hot_min) + 1
@@ -475,8 +486,10 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
     ids_int64 = 0;
     topk_w = route->out_w;
   }
-  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4, DSV4_ERR_UNSUPPORTED,
-          "layer: unknown profile %d", profile);
+  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4 || profile == DSV4_PROFILE_BF16_PURE,
+          DSV4_ERR_UNSUPPORTED, "layer: unknown profile %d", profile);
+  REQUIRE(profile != DSV4_PROFILE_BF16_PURE || !shared, DSV4_ERR_UNSUPPORTED,
+          "layer: the fused shared expert needs the bf16 profile with its FP8 round trips");
   REQUIRE(T >= 0 && K > 0 && K <= DSV4_MAX_TOPK, DSV4_ERR_SHAPE, "layer: bad T=%d K=%d", T, K);
   REQUIRE(D % 512 == 0 && I % 512 == 0 && D > 0 && I > 0, DSV4_ERR_UNSUPPORTED,
           "layer: D=%d and I=%d must be multiples of 512", D, I);
@@ -496,11 +509,13 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
   const int Rt = R + n_sh;
   const int bm = w.bm;
   REQUIRE(E > 0 && E <= DSV4_MAX_EXPERTS, DSV4_ERR_UNSUPPORTED, "layer: E=%d outside 1..%d", E, DSV4_MAX_EXPERTS);
-  REQUIRE(scale_rule == DSV4_RULE_CEIL_DIV6 || scale_rule == DSV4_RULE_OCP_FLOOR || profile == DSV4_PROFILE_BF16,
+  REQUIRE(scale_rule == DSV4_RULE_CEIL_DIV6 || scale_rule == DSV4_RULE_OCP_FLOOR || profile != DSV4_PROFILE_A4W4,
           DSV4_ERR_UNSUPPORTED, "layer: unknown scale rule %d", scale_rule);
   REQUIRE(aligned(x, 16), DSV4_ERR_SHAPE, "layer: x not 16-byte aligned");
   const bool fp8 = profile == DSV4_PROFILE_BF16;
-  const int afmt = fp8 ? DSV4_AFMT_E4M3 : DSV4_AFMT_E2M1;
+  const bool pure = profile == DSV4_PROFILE_BF16_PURE;  // x and h stay bf16: no quantisation launches
+  const int afmt = fp8 ? DSV4_AFMT_E4M3 : pure ? DSV4_AFMT_BF16 : DSV4_AFMT_E2M1;
+  const int64_t x_elems = pure ? 0 : (int64_t)T * D;  // the align launch quantises x unless pure
   REQUIRE(moe_gemm_supported_kdim(D) && moe_gemm_supported_kdim(I), DSV4_ERR_UNSUPPORTED,
           "layer: no GEMM compiled for D=%d / I=%d", D, I);
   // routing layout and the activation quantisation of x share one launch
@@ -518,9 +533,9 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
                            route->input_ids, route->ids_is64, route->vocab, route->renorm, route->scale,
                            route->out_w, route->out_ids, route->status};
     if (T <= kFusedRouteTokens && R <= kAlignSmallRows) {  // top-k, align and x quantisation in one launch
-      rc = hip_status(launch_route_align_quant(ra, bm, w.max_blocks, ao, (const uint16_t*)x, (int64_t)T * D,
-                                               fp8 ? 0 : 1, scale_rule, base + w.xa, base + w.xs,
-                                               (hipStream_t)stream, n_sh),
+      rc = hip_status(launch_route_align_quant(ra, bm, w.max_blocks, ao, pure ? nullptr : (const uint16_t*)x,
+                                               x_elems, fp8 ? 0 : 1, scale_rule, pure ? nullptr : base + w.xa,
+                                               pure ? nullptr : base + w.xs, (hipStream_t)stream, n_sh),
                       "route+align+quant launch");
       aligned_already = true;
     } else {
@@ -534,23 +549,25 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
                        (int32_t*)(base + w.npp_h)};
   if (!aligned_already) rc = hip_status(
       R > kAlignSmallRows
-          ? launch_moe_align_chunked(topk_ids, ids_int64, nullptr, R, K, E, bm, w.max_blocks, ao, (const uint16_t*)x,
-                                     (int64_t)T * D, fp8 ? 0 : 1, scale_rule, base + w.xa, base + w.xs,
+          ? launch_moe_align_chunked(topk_ids, ids_int64, nullptr, R, K, E, bm, w.max_blocks, ao,
+                                     pure ? nullptr : (const uint16_t*)x, x_elems, fp8 ? 0 : 1, scale_rule,
+                                     pure ? nullptr : base + w.xa, pure ? nullptr : base + w.xs,
                                      (hipStream_t)stream, n_sh, base + w.align_scratch,
                                      w.hot_min > 0 ? &hot : nullptr)
-          : launch_moe_align_quant(topk_ids, ids_int64, nullptr, R, K, E, bm, w.max_blocks, ao, (const uint16_t*)x,
-                                   (int64_t)T * D, fp8 ? 0 : 1, scale_rule, base + w.xa, base + w.xs,
+          : launch_moe_align_quant(topk_ids, ids_int64, nullptr, R, K, E, bm, w.max_blocks, ao,
+                                   pure ? nullptr : (const uint16_t*)x, x_elems, fp8 ? 0 : 1, scale_rule,
+                                   pure ? nullptr : base + w.xa, pure ? nullptr : base + w.xs,
                                    (hipStream_t)stream, n_sh),
       "align+quant launch");
   if (rc) return rc;
   const Dsv4ExpertPtrs* table = (const Dsv4ExpertPtrs*)expert_table;
   // gate/up + SwiGLU, quantising h in the epilogue where the kernel holds whole blocks
-  const bool hq_fused = !fp8 || bm != DSV4_GEMM_BLOCK_M;
+  const bool hq_fused = !pure && (!fp8 || bm != DSV4_GEMM_BLOCK_M);
   Dsv4GemmArgs gu{};
   gu.afmt = afmt;
-  gu.a = (const uint8_t*)(base + w.xa);
-  gu.a_row_bytes = fp8 ? (int64_t)D : (int64_t)D / 2;
-  gu.a_scale = (const uint8_t*)(base + w.xs);
+  gu.a = pure ? (const uint8_t*)x : (const uint8_t*)(base + w.xa);
+  gu.a_row_bytes = a_row_bytes(afmt, D);
+  gu.a_scale = pure ? nullptr : (const uint8_t*)(base + w.xs);
   gu.a_row_div = K;
   gu.sorted_ids = sorted_ids;
   gu.block_expert = block_expert;
@@ -593,15 +610,15 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
     rc = hip_status(launch_moe_gemm_gateup(hot_args(gu), (hipStream_t)stream), "gemm gate/up (large tiles) launch");
     if (rc) return rc;
   }
-  if (!hq_fused) {  // FP8 blocks of 128 columns span four single-wave workgroups
+  if (!hq_fused && !pure) {  // FP8 blocks of 128 columns span four single-wave workgroups
     rc = dsv4_fp8_act_quant(base + w.h, Rt, I, 128, nullptr, base + w.ha, nullptr, base + w.hs, stream);
     if (rc) return rc;
   }
   Dsv4GemmArgs dn{};
   dn.afmt = afmt;
-  dn.a = (const uint8_t*)(base + w.ha);
-  dn.a_row_bytes = fp8 ? (int64_t)I : (int64_t)I / 2;
-  dn.a_scale = (const uint8_t*)(base + w.hs);
+  dn.a = (const uint8_t*)(base + (pure ? w.h : w.ha));
+  dn.a_row_bytes = a_row_bytes(afmt, I);
+  dn.a_scale = pure ? nullptr : (const uint8_t*)(base + w.hs);
   dn.a_row_div = 1;
   dn.sorted_ids = sorted_ids;
   dn.block_expert = block_expert;
@@ -635,7 +652,8 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
 int dsv4_moe_layer_workspace_bytes(int T, int K, int E, int D, int I, int profile, int64_t* bytes) {
   REQUIRE(bytes, DSV4_ERR_NULL, "workspace: null output");
   REQUIRE(T >= 0 && K > 0 && E > 0 && D > 0 && I > 0, DSV4_ERR_SHAPE, "workspace: bad sizes");
-  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4, DSV4_ERR_UNSUPPORTED,
+  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4 || profile == DSV4_PROFILE_BF16_PURE,
+          DSV4_ERR_UNSUPPORTED,
           "workspace: unknown profile %d", profile);
   *bytes = layer_ws(T, K, E, D, I, profile).total;
   return DSV4_OK;
@@ -698,8 +716,8 @@ static int scratch_address(void* stream, void** out) {
 int dsv4_moe_layer_forward_noalloc(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
                                    const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
                                    float swiglu_limit, void* y, void* stream) {
-  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4, DSV4_ERR_UNSUPPORTED,
-          "no-alloc layer: unknown profile %d", profile);
+  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4 || profile == DSV4_PROFILE_BF16_PURE,
+          DSV4_ERR_UNSUPPORTED, "no-alloc layer: unknown profile %d", profile);
   REQUIRE(T >= 0 && K > 0 && K <= DSV4_MAX_TOPK && E > 0 && D > 0 && I > 0, DSV4_ERR_SHAPE,
           "no-alloc layer: bad sizes T=%d K=%d E=%d D=%d I=%d", T, K, E, D, I);
   if (T == 0) return DSV4_OK;
@@ -752,8 +770,8 @@ int dsv4_moe_routed_layer_workspace_bytes(int T, int K, int E, int D, int I, int
                                           int64_t* bytes) {
   REQUIRE(bytes, DSV4_ERR_NULL, "workspace: null output");
   REQUIRE(T >= 0 && K > 0 && E > 0 && D > 0 && I > 0, DSV4_ERR_SHAPE, "workspace: bad sizes");
-  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4, DSV4_ERR_UNSUPPORTED,
-          "workspace: unknown profile %d", profile);
+  REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4 || profile == DSV4_PROFILE_BF16_PURE,
+          DSV4_ERR_UNSUPPORTED, "workspace: unknown profile %d", profile);
   *bytes = layer_ws(T, K, E, D, I, profile, with_shared != 0, true).total;
   return DSV4_OK;
 }

@@ -83,6 +83,13 @@ struct AStage<1> {  // E2M1: 16 bytes per lane per MFMA
   v4i d[2];
   uint32_t s;
 };
+// bf16 activations (kAfmtBf16): for scaled-MFMA position ji, the lane's 32 bf16 of the
+// 32-k block its weight chunk covers, as 4 x 16 bytes (one bf16 MFMA each)
+template <>
+struct AStage<kAfmtBf16> {
+  v4i d[2][4];
+  uint32_t s;
+};
 // B operand of one stage: E2M1 weights (16 bytes per lane per MFMA, kNT tiles)
 // or, for the shared expert, E4M3 weights (32 bytes, laid out like the E4M3 A
 // operand). An E4M3 stage holds kNT/2 tiles, so both take the same registers;
@@ -169,7 +176,14 @@ DSV4_DEV uint32_t stage_scales(const RowScales<NST>& rs, int j, int r16, int g) 
 
 template <int AFMT, bool SCALES = true>
 DSV4_DEV void load_a(AStage<AFMT>& a, const uint8_t* abase, const uint8_t* asbase, int j, int g) {
-  if constexpr (AFMT == 1) {
+  if constexpr (AFMT == kAfmtBf16) {  // k block 8j + 2g + ji: elements 256j + 64g + 32ji .. +32
+    const uint8_t* p = abase + (int64_t)j * 512 + 128 * g;
+#pragma unroll
+    for (int ji = 0; ji < 2; ++ji)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) a.d[ji][m] = ld16(p + 64 * ji + 16 * m);
+    return;
+  } else if constexpr (AFMT == 1) {
     const uint8_t* p = abase + (int64_t)j * 128 + g * 32;
     a.d[0] = ld16(p);
     a.d[1] = ld16(p + 16);
@@ -260,6 +274,37 @@ DSV4_DEV void compute(v4f* acc, const AStage<AFMT>& a, const BStageT<B8>& b) {
   }
 }
 
+// bf16 activations: the lane's E2M1 chunk of weight row r16 for MFMA position ji holds
+// the 32 k its A data holds (low nibble first), so each 4-byte word m of the chunk, with
+// the row's E8M0 applied by the scaled convert (exact: at most two significant bits),
+// is the B operand of the bf16 MFMA whose A operand is A word m: both sides feed the
+// same 8 k's in the same lane positions, which is all the k pairing of the MFMA needs.
+// (The convert decodes nibble 8 to -0, harmless in a product; a scale byte of 255 gives
+// non-finite weights, as the reference's dequant does.)
+template <bool B8>
+DSV4_DEV void compute_bf16(v4f* acc, const AStage<kAfmtBf16>& a, const BStageT<B8>& b) {
+  static_assert(!B8, "bf16 activations meet E2M1 weights only");
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int ji = 0; ji < 2; ++ji)
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) {
+      const float sc = dsv4::e8m0_to_f32((b.s[t] >> (8 * ji)) & 0xffu);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const uint32_t w = (uint32_t)b.d[t][ji][m];
+        const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0);
+        const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1);
+        const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2);
+        const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3);
+        const bf16x8 bw = bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a.d[ji][m]), bw, acc[t], 0, 0,
+                                                         0);
+      }
+    }
+}
+
 // A row of flat index f: a routed entry reads row f / a_row_div, one of the
 // trailing shared_a_rows shared-expert entries row f - (R - shared_a_rows), and
 // padding (f >= R) row 0 (its products land only in rows that are never stored).
@@ -347,7 +392,7 @@ __attribute__((always_inline)) DSV4_DEV void moe_gemm_block(const Dsv4GemmArgs& 
   // A operand row of this lane, gathered on load
   const int64_t arow = a_row<SH>(p, p.sorted_ids[mb * kBM + r16]);
   const uint8_t* abase = p.a + arow * p.a_row_bytes;
-  const uint8_t* asbase = p.a_scale + arow * (int64_t)(p.Kdim / 32);
+  const uint8_t* asbase = AFMT == kAfmtBf16 ? nullptr : p.a_scale + arow * (int64_t)(p.Kdim / 32);
 
   // weight rows of this lane's tiles (E2M1: K/2 bytes per row, E4M3: K)
   const int64_t brow_bytes = shared ? p.Kdim : p.Kdim / 2, bsrow = p.Kdim / 32;
@@ -403,7 +448,7 @@ __attribute__((always_inline)) DSV4_DEV void moe_gemm_block(const Dsv4GemmArgs& 
     AStage<AFMT> a[RING];
     BStageT<B8> b[RING];
     RowScales<NST> as_row, bs_row[NTB];
-    load_row_scales<NST>(as_row, asbase, g);
+    if constexpr (AFMT != kAfmtBf16) load_row_scales<NST>(as_row, asbase, g);
 #pragma unroll
     for (int t = 0; t < NTB; ++t) load_row_scales<NST>(bs_row[t], bstp[t], g);
 #pragma unroll
@@ -418,10 +463,14 @@ __attribute__((always_inline)) DSV4_DEV void moe_gemm_block(const Dsv4GemmArgs& 
         load_b<false, B8, NT>(b[(j + P) % RING], btp, bstp, j + P, g, lay);
       }
       if constexpr (P > 0) __builtin_amdgcn_sched_barrier(0);
-      a[j % RING].s = stage_scales<NST>(as_row, j, r16, g);
 #pragma unroll
       for (int t = 0; t < NTB; ++t) b[j % RING].s[t] = stage_scales<NST>(bs_row[t], j, r16, g);
-      compute<AFMT, B8>(acc + t0, a[j % RING], b[j % RING]);
+      if constexpr (AFMT == kAfmtBf16) {
+        compute_bf16<B8>(acc + t0, a[j % RING], b[j % RING]);
+      } else {
+        a[j % RING].s = stage_scales<NST>(as_row, j, r16, g);
+        compute<AFMT, B8>(acc + t0, a[j % RING], b[j % RING]);
+      }
       if constexpr (P > 0) __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -705,6 +754,12 @@ static void launch_nst_sh(const Dsv4GemmArgs& a, hipStream_t st) {
   const int cols_per_wave = GATEUP ? 32 : 64;
   if (a.block_m == kBM) {  // decode-shaped: single-wave workgroups
     const dim3 grid(a.N / (kWaves * cols_per_wave), a.max_blocks);
+    if constexpr (!SH) {  // bf16 activations: routed experts only
+      if (a.afmt == kAfmtBf16) {
+        hipLaunchKernelGGL((moe_gemm_kernel<kAfmtBf16, GATEUP, NST, false>), grid, dim3(64 * kWaves), 0, st, a);
+        return;
+      }
+    }
     if (a.afmt == 0)
       hipLaunchKernelGGL((moe_gemm_kernel<0, GATEUP, NST, SH>), grid, dim3(64 * kWaves), 0, st, a);
     else
@@ -741,6 +796,8 @@ template <bool GATEUP>
 static hipError_t launch(const Dsv4GemmArgs& a, hipStream_t st) {
   if (a.block_m == kHotBlockM && !a.has_shared) return launch_moe_gemm_big(a, GATEUP, st);  // gemm_big.hip
   if (a.block_m != 16 && a.block_m != 64 && a.block_m != 128) return hipErrorInvalidValue;
+  // bf16 activations: the 16-row kernel only, without a shared expert or a fused h quantisation
+  if (a.afmt == kAfmtBf16 && (a.block_m != 16 || a.has_shared || (GATEUP && a.hq_mode))) return hipErrorInvalidValue;
   switch (a.Kdim / kStageK) {
     case 2: launch_nst<GATEUP, 2>(a, st); break;
     case 4: launch_nst<GATEUP, 4>(a, st); break;

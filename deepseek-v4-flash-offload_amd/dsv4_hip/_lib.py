@@ -14,8 +14,10 @@ LIB_PATH = os.path.join(_HERE, "libdsv4hip.so")
 DSV4_OK = 0
 AFMT_E4M3 = 0
 AFMT_E2M1 = 1
+AFMT_BF16 = 2  # bf16 rows as they are, bf16 MFMA on the dequantised weights; block_m 16 only
 PROFILE_BF16 = 0
 PROFILE_A4W4 = 1
+PROFILE_BF16_PURE = 2  # the bf16 profile without the FP8 round trips of x and h
 RULE_CEIL_DIV6 = 0
 RULE_OCP_FLOOR = 1
 SCORING = {"softmax": 0, "sigmoid": 1, "sqrtsoftplus": 2}

@@ -49,6 +49,11 @@ v4 = _find_v4()
 
 _PATCHED = False
 _MXFP4_GMM = os.environ.get("DSV4_MXFP4_GMM", "0") == "1"
+# The bf16 profile's per-128 FP8 round trips of x and h (deepseek_v4.py:170,188),
+# as the reference does; False runs the pure-bf16 variant (bf16 x and h against
+# the bf16-dequantised weights, fp32 accumulation). Read at call time; env
+# DSV4_FP8_ROUNDTRIP=0 turns them off.
+_FP8_ROUNDTRIP = os.environ.get("DSV4_FP8_ROUNDTRIP", "1") != "0"
 # activation scale rule of the a4w4 profile: "ocp_floor" or "ceil_div6"
 _MX_RULE = os.environ.get("DSV4_MX_RULE", "ocp_floor")
 _RULES = {"ocp_floor": _lib.RULE_OCP_FLOOR, "ceil_div6": _lib.RULE_CEIL_DIV6}
@@ -247,9 +252,12 @@ class OffloadDeepseekV4MoE(_BASE):
         rule = _RULES[_MX_RULE]
         limit = self.swiglu_limit if (self.swiglu_limit and self.swiglu_limit > 0) else 0.0
         fp8 = profile == _lib.PROFILE_BF16
+        pure = profile == _lib.PROFILE_BF16_PURE
         if fp8:
             q = _ops.fp8_act_quant(x, 128, want_codes=True, want_e8m0x4=True)
             xa, xs, afmt = q["codes"], q["e8m0x4"], _lib.AFMT_E4M3
+        elif pure:
+            xa, xs, afmt = x.contiguous(), None, _lib.AFMT_BF16
         else:
             xa, xs, _ = _ops.mxfp4_act_quant(x, rule)
             afmt = _lib.AFMT_E2M1
@@ -268,6 +276,8 @@ class OffloadDeepseekV4MoE(_BASE):
             if fp8:
                 q = _ops.fp8_act_quant(h, 128, want_codes=True, want_e8m0x4=True)
                 ha, has = q["codes"], q["e8m0x4"]
+            elif pure:
+                ha, has = h, None
             else:
                 ha, has, _ = _ops.mxfp4_act_quant(h, rule)
             _ops.gemm_down(afmt, ha, has, al, table, inter, D, out=out)
@@ -284,7 +294,8 @@ class OffloadDeepseekV4MoE(_BASE):
         profile when the module toggle ``_MXFP4_GMM`` is set (``:199-245``).
         ``shared`` (a prepared FP8 shared expert, bf16 profile) adds the shared
         expert's output computed in the same launches."""
-        profile = _lib.PROFILE_A4W4 if _MXFP4_GMM else _lib.PROFILE_BF16
+        profile = (_lib.PROFILE_A4W4 if _MXFP4_GMM else
+                   _lib.PROFILE_BF16 if _FP8_ROUNDTRIP else _lib.PROFILE_BF16_PURE)
         if hs.is_cuda and _FUSED_ROUTE and not _PREFETCH_NEXT:
             y = self._routed_resident(hs, input_ids, profile, shared)
             if y is not None:
@@ -315,7 +326,8 @@ class OffloadDeepseekV4MoE(_BASE):
         return y.type_as(hs)
 
     def _fused_shared(self, hs):
-        if not (_FUSE_SHARED and not _MXFP4_GMM and hs.is_cuda and hasattr(self.engine, "get_shared")):
+        if not (_FUSE_SHARED and not _MXFP4_GMM and _FP8_ROUNDTRIP and hs.is_cuda
+                and hasattr(self.engine, "get_shared")):
             return None
         return self.engine.get_shared(self.layer_idx, hs.device)
 

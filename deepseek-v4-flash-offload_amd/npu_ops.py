@@ -139,11 +139,12 @@ def grouped_matmul(x, weight, group_list, scale=None, per_token_scale=None, grou
     * bf16 ``[M, K]`` with ``fp8_roundtrip=True``: x is first replaced by its
       per-128 FP8 round trip (``act_quant(x, 128, "ue8m0", None, True)``), as
       the bf16 profile does before each of its grouped GEMMs
-      (``deepseek_v4.py:170,188``), and the product runs on the FP8 x FP4 MFMA.
-
-    A plain bf16 x (``npu_grouped_matmul(x=[bf16], weight=[bf16 w.t()])``)
-    without ``fp8_roundtrip`` raises: this entry point does not compute a
-    bf16 x bf16 product, and quantising x silently would change the numbers."""
+      (``deepseek_v4.py:170,188``), and the product runs on the FP8 x FP4 MFMA;
+    * bf16 ``[M, K]`` as it is (the default): ``x @ bf16(dequant(W))^T`` with
+      fp32 accumulation on the bf16 MFMA - the product
+      ``npu_grouped_matmul(x=[bf16], weight=[bf16 w.t()])`` computes on the
+      bf16-dequantised weights (``deepseek_v4.py:174-182``), no quantisation of
+      x."""
     if group_list_type != 1:
         raise NotImplementedError("grouped_matmul: group_list_type=1 (counts) only")
     if output_dtype != torch.bfloat16:
@@ -179,11 +180,13 @@ def grouped_matmul(x, weight, group_list, scale=None, per_token_scale=None, grou
         xsc = xsc.reshape(M, K // 32).view(torch.uint8).contiguous()
         afmt = _lib.AFMT_E2M1
     else:
-        if xs.dtype != torch.bfloat16 or not fp8_roundtrip:
+        if xs.dtype != torch.bfloat16:
             raise NotImplementedError(
-                "grouped_matmul: activations must be packed E2M1 with per_token_scale, or bf16 with "
-                "fp8_roundtrip=True (the bf16 profile's per-128 FP8 round trip); a bf16 x bf16 product is "
-                f"not computed here (x dtype {xs.dtype})")
-        q = _ops.fp8_act_quant(xs.contiguous(), 128, want_codes=True, want_e8m0x4=True)
-        xa, xsc, afmt = q["codes"], q["e8m0x4"], _lib.AFMT_E4M3
+                "grouped_matmul: activations must be packed E2M1 with per_token_scale, or bf16 "
+                f"(x dtype {xs.dtype})")
+        if fp8_roundtrip:
+            q = _ops.fp8_act_quant(xs.contiguous(), 128, want_codes=True, want_e8m0x4=True)
+            xa, xsc, afmt = q["codes"], q["e8m0x4"], _lib.AFMT_E4M3
+        else:  # bf16 x bf16-dequantised weights: the 16-row kernel's bf16 MFMA path
+            xa, xsc, afmt = xs.contiguous(), None, _lib.AFMT_BF16  # (the align's 16-row blocks)
     return _ops.gemm_down(afmt, xa, xsc, al, table, K, N)

@@ -22,13 +22,15 @@ import torch
 from oracle import mxfp4 as Q
 from oracle import moe as M
 from _parity import check_bound, elementwise_rel, gemm_bound, swiglu_bound
-from dsv4_hip import ops, synth, AFMT_E2M1, AFMT_E4M3, PROFILE_A4W4, PROFILE_BF16, RULE_OCP_FLOOR, RULE_CEIL_DIV6
+from dsv4_hip import (ops, synth, AFMT_E2M1, AFMT_E4M3, PROFILE_A4W4, PROFILE_BF16, PROFILE_BF16_PURE,
+                      RULE_OCP_FLOOR, RULE_CEIL_DIV6)
 
 pytestmark = pytest.mark.gpu
 
-TOL = {"bf16": 1e-2, "a4w4": 2e-2}
-# per-element relative error with a floor of rms(output) (_parity.elementwise_rel); a4w4: bit for bit
-ELEM_TOL = {"bf16": 5e-2, "a4w4": 0.0}
+TOL = {"bf16": 1e-2, "a4w4": 2e-2, "bf16_pure": 1e-2}
+# per-element relative error with a floor of rms(output) (_parity.elementwise_rel); a4w4: bit for bit;
+# the pure-bf16 variant has no quantisation step for a 1-ulp difference to move
+ELEM_TOL = {"bf16": 5e-2, "a4w4": 0.0, "bf16_pure": 2e-2}
 
 
 def rel(a, b):
@@ -163,22 +165,24 @@ def test_grouped_gemm_empty_group_pattern(gpu):
         assert rel(Q.bf16_bits_to_f32(_bits(h))[rows], ref) <= 1e-2
 
 
-@pytest.mark.parametrize("profile", ["bf16", "a4w4"])
+@pytest.mark.parametrize("profile", ["bf16", "a4w4", "bf16_pure"])
 @pytest.mark.parametrize("T,K,E,D,I", [(8, 8, 256, 4096, 2048), (64, 6, 32, 1024, 512), (100, 6, 32, 1024, 512),
                                        (256, 8, 32, 2048, 1024), (400, 8, 256, 1024, 512)])
 def test_layer_forward_vs_oracle(gpu, profile, T, K, E, D, I):
     # 16-row blocks up to 2047 routed rows (h quantised in the gate/up epilogue for a4w4,
     # by a separate launch for FP8); 256 tokens x top-8 = 2048 routed rows: 64-row M blocks
     # (tiled kernel, h quantised in the epilogue in both profiles); 3200 routed rows: the
-    # chunked two-launch align
+    # chunked two-launch align. The pure-bf16 variant runs 16-row blocks at every size.
     ids, w, xb, host, devw, table = _case(T, K, E, D, I, 77 + T, gpu)
     runner = ops.LayerRunner(gpu, E, D, I)
     x = _dev_bf16(xb, gpu)
-    prof = PROFILE_BF16 if profile == "bf16" else PROFILE_A4W4
+    prof = {"bf16": PROFILE_BF16, "a4w4": PROFILE_A4W4, "bf16_pure": PROFILE_BF16_PURE}[profile]
     y = runner.forward(x, _dev(ids, gpu), _dev(w, gpu), table, profile=prof, rule=RULE_OCP_FLOOR)
     torch.cuda.synchronize()
     if profile == "bf16":
         ref = M.routed_bf16(xb, ids, w, host, n_experts=E)
+    elif profile == "bf16_pure":
+        ref = M.routed_bf16(xb, ids, w, host, n_experts=E, fp8_act=False)
     else:
         ref = M.routed_a4w4(xb, ids, w, host, n_experts=E, rule="ocp_floor")
     got = Q.bf16_bits_to_f32(_bits(y))
@@ -201,3 +205,91 @@ def test_layer_forward_ceil_rule_and_int32_ids(gpu):
     torch.cuda.synchronize()
     ref = M.routed_a4w4(xb, ids, w, host, n_experts=E, rule="ceil_div6")
     assert rel(Q.bf16_bits_to_f32(_bits(y)), Q.bf16_bits_to_f32(ref["y"])) <= TOL["a4w4"]
+
+
+# ---- the pure-bf16 variant: bf16 activations as they are on the bf16 MFMA ----
+# Products of a bf16 value and an exactly dequantised E2M1 weight are exact in fp32 and
+# the MFMA accumulates in fp32, so each output is within one bf16 ulp of the float64
+# oracle plus 2^-16 of its sum of absolute products (fp32 summation over K <= 4096).
+PURE_ACC_REL = 2.0 ** -16
+
+
+@pytest.mark.parametrize("T,K,E,D,I", [(24, 4, 16, 1024, 512), (8, 8, 256, 4096, 2048), (200, 8, 16, 512, 512)])
+def test_grouped_gemm_stages_bf16_pure(gpu, T, K, E, D, I):
+    from dsv4_hip import AFMT_BF16
+    ids, w, xb, host, devw, table = _case(T, K, E, D, I, 71 + T, gpu)
+    al = ops.moe_align(_dev(ids, gpu), _dev(w, gpu), E, 16)
+    R = T * K
+    x = _dev_bf16(xb, gpu)
+    h = ops.gemm_gateup(AFMT_BF16, x, None, K, al, table, D, I, _dev(w.reshape(-1), gpu), 10.0)
+    torch.cuda.synchronize()
+    a_f = Q.bf16_bits_to_f32(xb)
+    flat_e = ids.reshape(-1)
+    h_ref = np.zeros((R, I), np.float32)
+    g_all, u_all = np.zeros((R, I), np.float32), np.zeros((R, I), np.float32)
+    g_abs, u_abs = np.zeros((R, I), np.float32), np.zeros((R, I), np.float32)
+    for e in np.unique(flat_e):
+        rows = np.nonzero(flat_e == e)[0]
+        w1 = Q.dequant_fp4_weight_f32(host[e]["w1p"], host[e]["w1s"])
+        w3 = Q.dequant_fp4_weight_f32(host[e]["w3p"], host[e]["w3s"])
+        xa = a_f[rows // K]
+        g = Q.f32_to_bf16_f32(M.matmul_nt(xa, w1))
+        u = Q.f32_to_bf16_f32(M.matmul_nt(xa, w3))
+        g_all[rows], u_all[rows] = g, u
+        g_abs[rows], u_abs[rows] = M.matmul_nt(np.abs(xa), np.abs(w1)), M.matmul_nt(np.abs(xa), np.abs(w3))
+        h_ref[rows] = M.swiglu(g, u, w.reshape(-1)[rows], 10.0)
+    h_gpu = Q.bf16_bits_to_f32(_bits(h))
+    h_want = Q.f32_to_bf16_f32(h_ref)
+    print(f"pure bf16 gate/up T={T}: normwise rel {rel(h_gpu, h_want):.3e}")
+    check_bound(h_gpu, h_want, swiglu_bound(g_all, u_all, w.reshape(-1), 10.0, h_want, g_abs, u_abs,
+                                            acc_rel=PURE_ACC_REL), f"pure bf16 gate/up T={T}")
+    # down on the oracle's bf16 h, as it is
+    hb = Q.f32_to_bf16_bits(h_ref)
+    out = ops.gemm_down(AFMT_BF16, _dev_bf16(hb, gpu), None, al, table, I, D)
+    torch.cuda.synchronize()
+    hf = Q.bf16_bits_to_f32(hb)
+    out_ref = np.zeros((R, D), np.float32)
+    out_abs = np.zeros((R, D), np.float32)
+    for e in np.unique(flat_e):
+        rows = np.nonzero(flat_e == e)[0]
+        w2 = Q.dequant_fp4_weight_f32(host[e]["w2p"], host[e]["w2s"])
+        out_ref[rows] = M.matmul_nt(hf[rows], w2)
+        out_abs[rows] = M.matmul_nt(np.abs(hf[rows]), np.abs(w2))
+    out_gpu, out_want = Q.bf16_bits_to_f32(_bits(out)), Q.f32_to_bf16_f32(out_ref)
+    print(f"pure bf16 down T={T}: normwise rel {rel(out_gpu, out_want):.3e}")
+    check_bound(out_gpu, out_want, gemm_bound(out_want, out_abs, acc_rel=PURE_ACC_REL), f"pure bf16 down T={T}")
+
+
+def test_dequant_in_the_bf16_gemm_every_byte_and_scale(gpu):
+    # one-hot activations pick single weight elements: out[f][n] = W[n][k(f)] exactly, so
+    # every packed byte value with every E8M0 byte 0..252 goes through the GEMM's
+    # dequantisation and must equal the oracle's bf16 dequant (up to the sign of zero).
+    # Above 252 some weights are infinite, and 0 x inf would turn whole output columns
+    # into NaN, as it does in any dot product with them.
+    from dsv4_hip import AFMT_BF16
+    D, I, E = 512, 512, 1
+    rng = np.random.default_rng(5)
+    w2p = rng.integers(0, 256, (D, I // 2), dtype=np.uint8)
+    w2s = np.tile(np.arange(253, dtype=np.uint8), (D * (I // 32)) // 253 + 1)[:D * (I // 32)].reshape(D, I // 32)
+    rng.shuffle(w2s.reshape(-1))
+    ex = {k: torch.zeros(16, dtype=torch.uint8, device=gpu) for k in ("w1p", "w1s", "w3p", "w3s")}
+    ex["w2p"], ex["w2s"] = _dev(w2p, gpu), _dev(w2s, gpu)
+    table = ops.expert_table({0: ex}, E, gpu)
+    R = I  # row f picks k = f
+    ids = np.zeros((R, 1), np.int64)
+    al = ops.moe_align(_dev(ids, gpu), None, E, 16)
+    one = np.zeros((R, I), np.float32)
+    one[np.arange(R), np.arange(R)] = 1.0
+    out = ops.gemm_down(AFMT_BF16, _dev_bf16(Q.f32_to_bf16_bits(one), gpu), None, al, table, I, D)
+    torch.cuda.synchronize()
+    want = Q.dequant_fp4_weight_f32(w2p, w2s).T   # [k, n]
+    got = Q.bf16_bits_to_f32(_bits(out))
+    assert np.isfinite(want).all()
+    bad = got != want
+    if bad.any():
+        k, n = np.nonzero(bad)
+        sb = w2s[n, k // 32]
+        print(f"{int(bad.sum())} differ; scale bytes {np.unique(sb)[:20]}; |want| max {np.abs(want[bad]).max():.3e}; "
+              f"got {got[bad][:8]} want {want[bad][:8]}")
+    assert not bad.any(), "dequantised weights differ"
+    print(f"{want.size} weight elements checked, scale bytes 0..252")

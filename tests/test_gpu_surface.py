@@ -16,6 +16,7 @@ from oracle import mxfp4 as Q
 from oracle import moe as M
 from oracle import routing as RT
 from dsv4_hip import synth
+from _parity import check_bound, gemm_bound
 
 pytestmark = pytest.mark.gpu
 
@@ -106,7 +107,7 @@ def test_npu_ops_align_permute_unpermute(gpu):
     assert np.array_equal(_bits(y), want)
 
 
-@pytest.mark.parametrize("form", ["a4w4_list", "a4w4_stacked_view", "bf16_x"])
+@pytest.mark.parametrize("form", ["a4w4_list", "a4w4_stacked_view", "bf16_x", "bf16_x_pure"])
 def test_npu_ops_grouped_matmul_groups_2_0_3(gpu, form):
     # _bench_gmm.py:8-22 group pattern, MXFP4 weights [N, K/2]
     counts, N, Kd = [2, 0, 3], 256, 512
@@ -119,9 +120,11 @@ def test_npu_ops_grouped_matmul_groups_2_0_3(gpu, form):
         a_f = Q.bf16_bits_to_f32(rt)
         kw = dict(weight=[torch.from_numpy(w).to(gpu) for w, _ in wts],
                   scale=[torch.from_numpy(s).to(gpu) for _, s in wts], group_list=counts)
-        with pytest.raises(NotImplementedError, match="fp8_roundtrip"):
-            npu_ops.grouped_matmul(x=[x.to(gpu)], **kw)          # no silent FP8 quantisation of bf16 x
         out = npu_ops.grouped_matmul(x=[x.to(gpu)], fp8_roundtrip=True, **kw)
+    elif form == "bf16_x_pure":  # bf16 x as it is against the bf16-dequantised weights
+        a_f = Q.bf16_bits_to_f32(xb)
+        out = npu_ops.grouped_matmul(x=[x.to(gpu)], weight=[torch.from_numpy(w).to(gpu) for w, _ in wts],
+                                     scale=[torch.from_numpy(s).to(gpu) for _, s in wts], group_list=counts)
     else:
         _, xp, xs = Q.ocp_mx_quant(xb, 32)
         a_f = Q.fp4_codes_to_f32(xp, xs)
@@ -139,8 +142,14 @@ def test_npu_ops_grouped_matmul_groups_2_0_3(gpu, form):
     o = 0
     for (w, s), c in zip(wts, counts):
         if c:
-            ref = M.matmul_nt(a_f[o:o + c], Q.dequant_fp4_weight_f32(w, s))
-            assert rel(got[o:o + c], ref) <= (2e-2 if form != "bf16_x" else 1e-2)
+            wf = Q.dequant_fp4_weight_f32(w, s)
+            ref = M.matmul_nt(a_f[o:o + c], wf)
+            assert rel(got[o:o + c], ref) <= (2e-2 if not form.startswith("bf16_x") else 1e-2)
+            if form == "bf16_x_pure":  # exact products, fp32 sums: one bf16 ulp + 2^-16 of sum |a b|
+                want = Q.f32_to_bf16_f32(ref)
+                check_bound(got[o:o + c], want,
+                            gemm_bound(want, M.matmul_nt(np.abs(a_f[o:o + c]), np.abs(wf)), acc_rel=2.0 ** -16),
+                            f"grouped_matmul pure bf16, group of {c}")
         o += c
 
 
@@ -265,6 +274,15 @@ def test_plugin_routed_matches_oracle(gpu, fast, is_hash):
     y = m._routed(x, ids)
     torch.cuda.synchronize()
     assert rel(Q.bf16_bits_to_f32(_bits(y)), Q.bf16_bits_to_f32(ref_b["y"])) <= 1e-2
+    # the pure-bf16 variant (no FP8 round trips of x and h) against the oracle's
+    saved = mod._FP8_ROUNDTRIP
+    mod._FP8_ROUNDTRIP = False
+    try:
+        yp = m._routed(x, ids)
+    finally:
+        mod._FP8_ROUNDTRIP = saved
+    ref_p = M.routed_bf16(xb, idx.cpu().numpy(), w.cpu().numpy(), host, n_experts=E, fp8_act=False)
+    assert rel(Q.bf16_bits_to_f32(_bits(yp)), Q.bf16_bits_to_f32(ref_p["y"])) <= 1e-2
     saved = mod._MXFP4_GMM
     mod._MXFP4_GMM = True
     try:
