@@ -308,8 +308,8 @@ static int check_gemm_common(int afmt, const void* a, const void* a_scale, const
                              const void* experts, int Kdim, void* out) {
   REQUIRE(afmt == DSV4_AFMT_E4M3 || afmt == DSV4_AFMT_E2M1 || afmt == DSV4_AFMT_BF16, DSV4_ERR_UNSUPPORTED,
           "gemm: unknown A format %d", afmt);
-  REQUIRE(afmt != DSV4_AFMT_BF16 || block_m == DSV4_GEMM_BLOCK_M, DSV4_ERR_UNSUPPORTED,
-          "gemm: bf16 activations need block_m %d (got %d)", DSV4_GEMM_BLOCK_M, block_m);
+  REQUIRE(afmt != DSV4_AFMT_BF16 || block_m == DSV4_GEMM_BLOCK_M || block_m == 64, DSV4_ERR_UNSUPPORTED,
+          "gemm: bf16 activations need block_m %d or 64 (got %d)", DSV4_GEMM_BLOCK_M, block_m);
   REQUIRE(R >= 0 && max_blocks >= 0, DSV4_ERR_SHAPE, "gemm: negative size");
   REQUIRE(moe_gemm_supported_kdim(Kdim), DSV4_ERR_UNSUPPORTED,
           "gemm: reduction dim %d unsupported (512, 1024, 2048 or 4096)", Kdim);
@@ -416,8 +416,8 @@ static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool sha
   LayerWs w{};
   const int64_t R = (int64_t)T * K;
   const int64_t Rt = R + (shared ? T : 0);  // routed rows, then the shared expert's T rows
-  const bool pure = profile == DSV4_PROFILE_BF16_PURE;  // bf16 x and h, the 16-row kernel only
-  const int bm = pure ? DSV4_GEMM_BLOCK_M : layer_block_m(R);
+  const bool pure = profile == DSV4_PROFILE_BF16_PURE;  // bf16 x and h (16- and 64-row kernels)
+  const int bm = layer_block_m(R);
   w.bm = bm;
   w.max_blocks = dsv4_moe_align_max_blocks((int)R, E, bm) + (shared ? (T + bm - 1) / bm : 0);
   const bool fp8 = profile == DSV4_PROFILE_BF16;

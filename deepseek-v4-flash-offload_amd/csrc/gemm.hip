@@ -565,20 +565,64 @@ DSV4_DEV void compute_tiled(v4f (*acc)[kNT], const uint8_t* lds, const uint8_t* 
   }
 }
 
+// bf16 activations (pure-bf16 variant), in two phases per 32-k half ji of a
+// stage: the weight fragments of the half are dequantised once (exactly, by
+// the hardware converter) into bw, then each feeds the MT row subtiles, whose
+// A fragments come from the LDS tile (rows of 512 bytes: the stage's 256 k).
+// Lane (r16, g) of MFMA (ji, m) takes the 8 k of 32-k block 2g + ji at offset
+// 8m, as in the 16-row kernel.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+DSV4_DEV void dequant_half(bf16x8_t (*bw)[4], const BStageT<false>& b, int ji) {
+#pragma unroll
+  for (int t = 0; t < kNT; ++t) {
+    const float sc = dsv4::e8m0_to_f32((b.s[t] >> (8 * ji)) & 0xffu);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t w = (uint32_t)b.d[t][ji][m];
+      const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0);
+      const bf16x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1);
+      const bf16x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2);
+      const bf16x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3);
+      bw[t][m] = bf16x8_t{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+    }
+  }
+}
+
+template <int MT>
+DSV4_DEV void mfma_half_bf16(v4f (*acc)[kNT], const uint8_t* lds, const bf16x8_t (*bw)[4], int ji, int r16, int g) {
+  constexpr int AROW = 512 + 16;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const uint8_t* ap = lds + (16 * mt + r16) * AROW + 64 * (2 * g + ji);
+    v4i a[4];
+#pragma unroll
+    for (int m = 0; m < 4; ++m) a[m] = *(const v4i*)(ap + 16 * m);
+#pragma unroll
+    for (int t = 0; t < kNT; ++t)
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        acc[mt][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a[m]), bw[t][m],
+                                                             acc[mt][t], 0, 0, 0);
+  }
+}
+
 template <int AFMT, bool GATEUP, int NST, int MT, int NW, bool SH>
 __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gemm_tiled_kernel(Dsv4GemmArgs p) {
   constexpr int BM = 16 * MT;
   constexpr int NTH = 64 * NW;                // threads per workgroup
-  constexpr int ASB = AFMT == 0 ? 256 : 128;  // A bytes per row per stage
+  constexpr bool ABF = AFMT == kAfmtBf16;     // bf16 activations: no A scales
+  constexpr int ASB = ABF ? 512 : AFMT == 0 ? 256 : 128;  // A bytes per row per stage
   constexpr int AROW = ASB + 16;              // padded LDS row stride
   constexpr int LV = BM * ASB / (NTH * 16);   // 16-byte A chunks one thread moves per stage
   constexpr int KSB = 8 * NST;                // scale bytes per row (K / 32)
   constexpr int ASP = KSB + 16;               // A scale table pitch: 16 rows on distinct banks
-  constexpr int AS_CHUNKS = BM * KSB / 16;
+  constexpr int AS_CHUNKS = ABF ? 0 : BM * KSB / 16;
   static_assert(LV >= 1 && LV * NTH * 16 == BM * ASB, "loader granularity");
   static_assert(NW % 4 == 0, "four gate/up waves make one 128-column FP8 block");
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][BM * AROW];
-  __shared__ __attribute__((aligned(16))) uint8_t as_tab[BM * ASP];
+  __shared__ __attribute__((aligned(16))) uint8_t as_tab[ABF ? 16 : BM * ASP];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int mb = blockIdx.y;
@@ -639,6 +683,57 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
 #pragma unroll
     for (int t = 0; t < kNT; ++t) acc[mt][t] = v4f{0.f, 0.f, 0.f, 0.f};
 
+  // bf16 activations: one weight stage in registers, whose half ji is reloaded
+  // with the next stage's as soon as it is dequantised; the weight rows' scale
+  // bytes come with each stage (a whole-K table per lane would not fit beside
+  // the dequantised fragments); the A tile moves in two halves (the other LDS
+  // buffer is free for the whole stage). Two waves per SIMD.
+  auto kloop_bf16 = [&](const uint8_t* const* btp, const uint8_t* const* bstp) {
+    static_assert(LV % 2 == 0, "the A tile moves in two halves");
+    constexpr int LH = LV / 2;
+    v4i lreg[LH];
+    BStageT<false> b;
+#pragma unroll
+    for (int v = 0; v < LV; ++v) *(v4i*)&a_lds[0][ldst[v]] = ld16(lsrc[v]);
+    load_b<false, false>(b, btp, bstp, 0, g, lay);
+#pragma unroll
+    for (int t = 0; t < kNT; ++t) b.s[t] = ld_u16(bstp[t] + 2 * g);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < NST; ++j) {
+      const bool more = j + 1 < NST;
+      uint8_t* nxt = a_lds[(j + 1) & 1];
+      if (more) {
+#pragma unroll
+        for (int v = 0; v < LH; ++v) lreg[v] = ld16(lsrc[v] + (j + 1) * ASB);
+      }
+      bf16x8_t bw[kNT][4];
+#pragma unroll
+      for (int ji = 0; ji < 2; ++ji) {
+        dequant_half(bw, b, ji);
+        if (more) {
+#pragma unroll
+          for (int t = 0; t < kNT; ++t) b.d[t][ji] = ld16_w<false>(btp[t] + (j + 1) * lay.stage_stride + ji * lay.mfma_stride);
+          if (ji == 1) {
+#pragma unroll
+            for (int t = 0; t < kNT; ++t) b.s[t] = ld_u16(bstp[t] + (j + 1) * 8 + 2 * g);
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_half_bf16<MT>(acc, a_lds[j & 1], bw, ji, r16, g);
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) {
+#pragma unroll
+          for (int v = 0; v < LH; ++v) *(v4i*)&nxt[ldst[ji * LH + v]] = lreg[v];
+          if (ji == 0) {
+#pragma unroll
+            for (int v = 0; v < LH; ++v) lreg[v] = ld16(lsrc[LH + v] + (j + 1) * ASB);
+          }
+        }
+      }
+      __syncthreads();
+    }
+  };
   // uniform per workgroup (have_w, shared), so the barriers inside are reached by all
   auto kloop = [&](auto b8, auto t0c) {
     constexpr bool B8 = decltype(b8)::value;
@@ -646,6 +741,10 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
     constexpr int NTB = BStageT<B8>::NTB;
     const uint8_t* const* btp = bt + t0;
     const uint8_t* const* bstp = bst + t0;
+    if constexpr (ABF) {
+      kloop_bf16(btp, bstp);
+      return;
+    }
     // scales of the whole K range, loaded once: the weight rows' by their lanes
     // (shared out per stage by permutes), the A rows' into an LDS table
     RowScales<NST> bs_row[NTB];
@@ -769,6 +868,12 @@ static void launch_nst_sh(const Dsv4GemmArgs& a, hipStream_t st) {
   // 4-wave workgroups (8-wave ones, sharing each A tile across twice the
   // columns, measured no faster)
   const dim3 grid(a.N / (4 * cols_per_wave), a.max_blocks);
+  if constexpr (!SH) {  // bf16 activations: 64-row blocks, routed experts only
+    if (a.afmt == kAfmtBf16) {
+      hipLaunchKernelGGL((moe_gemm_tiled_kernel<kAfmtBf16, GATEUP, NST, 4, 4, false>), grid, dim3(256), 0, st, a);
+      return;
+    }
+  }
   if (a.block_m == 64) {
     if (a.afmt == 0)
       hipLaunchKernelGGL((moe_gemm_tiled_kernel<0, GATEUP, NST, 4, 4, SH>), grid, dim3(256), 0, st, a);
@@ -796,8 +901,8 @@ template <bool GATEUP>
 static hipError_t launch(const Dsv4GemmArgs& a, hipStream_t st) {
   if (a.block_m == kHotBlockM && !a.has_shared) return launch_moe_gemm_big(a, GATEUP, st);  // gemm_big.hip
   if (a.block_m != 16 && a.block_m != 64 && a.block_m != 128) return hipErrorInvalidValue;
-  // bf16 activations: the 16-row kernel only, without a shared expert or a fused h quantisation
-  if (a.afmt == kAfmtBf16 && (a.block_m != 16 || a.has_shared || (GATEUP && a.hq_mode))) return hipErrorInvalidValue;
+  // bf16 activations: 16- or 64-row blocks, without a shared expert or a fused h quantisation
+  if (a.afmt == kAfmtBf16 && (a.block_m == 128 || a.has_shared || (GATEUP && a.hq_mode))) return hipErrorInvalidValue;
   switch (a.Kdim / kStageK) {
     case 2: launch_nst<GATEUP, 2>(a, st); break;
     case 4: launch_nst<GATEUP, 4>(a, st); break;

@@ -87,8 +87,8 @@ hipError_t launch_moe_unpermute_rows(const uint16_t* src, const int32_t* row, in
                                      int32_t* work_cnt, int32_t* work_pos, int32_t* status, uint16_t* y,
                                      hipStream_t st);
 
-// A format of the 16-row grouped GEMM only: bf16 activations (2 bytes/elt, row-major, no
-// a_scale) multiplied as they are - no FP8 round trip - against the exactly dequantised
+// A format of the 16- and 64-row grouped GEMMs: bf16 activations (2 bytes/elt, row-major,
+// no a_scale) multiplied as they are - no FP8 round trip - against the exactly dequantised
 // bf16 weights on the bf16 MFMA, fp32 accumulation (the "pure bf16" variant).
 constexpr int kAfmtBf16 = 2;
 

@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(_HERE, "libdsv4hip.so")
 DSV4_OK = 0
 AFMT_E4M3 = 0
 AFMT_E2M1 = 1
-AFMT_BF16 = 2  # bf16 rows as they are, bf16 MFMA on the dequantised weights; block_m 16 only
+AFMT_BF16 = 2  # bf16 rows as they are, bf16 MFMA on the dequantised weights; block_m 16 or 64
 PROFILE_BF16 = 0
 PROFILE_A4W4 = 1
 PROFILE_BF16_PURE = 2  # the bf16 profile without the FP8 round trips of x and h

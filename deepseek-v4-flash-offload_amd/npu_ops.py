@@ -173,7 +173,9 @@ def grouped_matmul(x, weight, group_list, scale=None, per_token_scale=None, grou
     table = _ops.expert_table({g: {"w1p": w, "w1s": s, "w2p": w, "w2s": s, "w3p": w, "w3s": s}
                                for g, (w, s) in enumerate(zip(ws, ss)) if counts[g]},
                               len(ws), dev)
-    al = _ops.moe_align(ids, None, len(ws))
+    # the layer's block rule: 16-row blocks (single-wave kernel) below 2048 rows,
+    # 64-row blocks (LDS-tiled kernel, weight fragments reused over 4 row tiles) above
+    al = _ops.moe_align(ids, None, len(ws), 64 if M >= 2048 else _lib.GEMM_BLOCK_M)
     if per_token_scale is not None:
         xa = xs.view(torch.uint8).contiguous()
         xsc = per_token_scale[0] if isinstance(per_token_scale, (list, tuple)) else per_token_scale
@@ -187,6 +189,6 @@ def grouped_matmul(x, weight, group_list, scale=None, per_token_scale=None, grou
         if fp8_roundtrip:
             q = _ops.fp8_act_quant(xs.contiguous(), 128, want_codes=True, want_e8m0x4=True)
             xa, xsc, afmt = q["codes"], q["e8m0x4"], _lib.AFMT_E4M3
-        else:  # bf16 x bf16-dequantised weights: the 16-row kernel's bf16 MFMA path
-            xa, xsc, afmt = xs.contiguous(), None, _lib.AFMT_BF16  # (the align's 16-row blocks)
+        else:  # bf16 x bf16-dequantised weights on the bf16 MFMA
+            xa, xsc, afmt = xs.contiguous(), None, _lib.AFMT_BF16
     return _ops.gemm_down(afmt, xa, xsc, al, table, K, N)

@@ -31,14 +31,14 @@ extern "C" {
 #define DSV4_AFMT_E4M3 0 /* one E4M3fn code per byte, E8M0 per 32 (bf16 profile) */
 #define DSV4_AFMT_E2M1 1 /* two E2M1 codes per byte, E8M0 per 32 (a4w4 profile) */
 #define DSV4_AFMT_BF16 2 /* bf16 rows as they are (a_scale unused), times the exactly dequantised \
-                            bf16 weights on the bf16 MFMA: the pure-bf16 variant; block_m 16 only */
+                            bf16 weights on the bf16 MFMA: the pure-bf16 variant; block_m 16 or 64 */
 
 /* profiles of the routed layer */
 #define DSV4_PROFILE_BF16 0 /* deepseek_v4.py:166-197 (FP8 round-trip activations) */
 #define DSV4_PROFILE_A4W4 1 /* deepseek_v4.py:199-245 (MXFP4 activations)          */
 #define DSV4_PROFILE_BF16_PURE 2 /* the bf16 profile without the FP8 round trips of x and h \
                                     (deepseek_v4.py:170,188 skipped): bf16 x bf16-dequantised \
-                                    weights, fp32 accumulation; 16-row blocks at every size */
+                                    weights, fp32 accumulation; 16-/64-row blocks as the others */
 
 /* MXFP4 activation scale rules */
 #define DSV4_RULE_CEIL_DIV6 0 /* 2^ceil(log2(amax/6)), npu_ops.py:107-121 */

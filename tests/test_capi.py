@@ -79,10 +79,13 @@ def test_gemm_and_layer_validation():
     rc, msg = _err(lib.dsv4_moe_gemm_down(3, None, None, None, None, None, 64, 16, 10, None, 2048, 4096, None,
                                           None))
     assert rc == -3 and "format" in msg
-    # bf16 activations (the pure-bf16 variant) only in the 16-row kernel
-    rc, msg = _err(lib.dsv4_moe_gemm_down(2, None, None, None, None, None, 64, 64, 10, None, 2048, 4096, None,
+    # bf16 activations (the pure-bf16 variant) only in the 16- and 64-row kernels
+    rc, msg = _err(lib.dsv4_moe_gemm_down(2, None, None, None, None, None, 64, 128, 10, None, 2048, 4096, None,
                                           None))
     assert rc == -3 and "bf16 activations" in msg
+    rc, msg = _err(lib.dsv4_moe_gemm_down(2, None, None, None, None, None, 64, 64, 10, None, 2048, 4096, None,
+                                          None))
+    assert rc == -1 and "null" in msg
     n = ctypes.c_int64(0)
     assert lib.dsv4_moe_layer_workspace_bytes(2048, 8, 256, 4096, 2048, 2, ctypes.byref(n)) == 0
     assert lib.dsv4_moe_layer_workspace_bytes(8, 8, 256, 4096, 2048, 3, ctypes.byref(n)) == -3

@@ -10,21 +10,24 @@ hidden 4096, inter 2048, at
 * 16384 tokens in both profiles: 131,072 routed rows; experts with at least 256
   rows (the Zipf-hot ones, up to ~14,000 rows) run in 256-row blocks on the
   large-tile kernel, the others in 64-row blocks;
-* 64 tokens in the a4w4 profile: 512 routed rows on the 16-row kernel.
+* 64 tokens in the a4w4 profile: 512 routed rows on the 16-row kernel;
+* 2048 tokens in the pure-bf16 variant (no FP8 round trips): 64-row blocks on
+  the tiled kernel with bf16 activations.
 Expert weights are random bytes generated on the device and stored MFMA-tiled,
 as the slot cache stores them. The oracle reads checkpoint-layout copies of the
 sampled tokens' experts. The sample at 2048 tokens: the tokens of the first and
 last routed row of every M block of the 16 hottest experts (the block edges of
 every hot expert; ~260 tokens) plus 32 random ones; at 16384 tokens the same for
 the 8 hottest experts in their 256-row blocks; at 64 tokens, all of them.
-Tolerances: max relative error (normwise) 1e-2 for bf16, 2e-2 for a4w4; per
-element, bf16 within 5e-2 of max(|ref|, rms(ref)) and a4w4 bit for bit."""
+Tolerances: max relative error (normwise) 1e-2 for bf16 and pure bf16, 2e-2 for
+a4w4; per element, bf16 within 5e-2 and pure bf16 within 2e-2 of
+max(|ref|, rms(ref)), a4w4 bit for bit."""
 
 import numpy as np
 import pytest
 import torch
 
-from dsv4_hip import ops, synth, PROFILE_A4W4, PROFILE_BF16, RULE_OCP_FLOOR
+from dsv4_hip import ops, synth, PROFILE_A4W4, PROFILE_BF16, PROFILE_BF16_PURE, RULE_OCP_FLOOR
 from oracle import moe as M
 from oracle import mxfp4 as Q
 from _parity import elementwise_rel
@@ -32,8 +35,9 @@ from _parity import elementwise_rel
 pytestmark = pytest.mark.gpu
 
 E, K, D, I = 256, 8, 4096, 2048
-TOL = {"bf16": 1e-2, "a4w4": 2e-2}
-ELEM_TOL = {"bf16": 5e-2, "a4w4": 0.0}  # per element, floor rms(ref) (_parity.elementwise_rel); a4w4 exact
+TOL = {"bf16": 1e-2, "a4w4": 2e-2, "bf16_pure": 1e-2}
+# per element, floor rms(ref) (_parity.elementwise_rel); a4w4 exact
+ELEM_TOL = {"bf16": 5e-2, "a4w4": 0.0, "bf16_pure": 2e-2}
 
 
 def _bits(t):
@@ -54,7 +58,7 @@ def _device_experts(dev, seed):
 
 
 @pytest.mark.parametrize("profile,T", [("bf16", 2048), ("a4w4", 2048), ("a4w4", 64), ("bf16", 16384),
-                                       ("a4w4", 16384)])
+                                       ("a4w4", 16384), ("bf16_pure", 2048)])
 def test_full_size_layer_on_sampled_tokens(gpu, profile, T):
     ids = synth.zipf_topk(T, K, E, synth.rank_permutation(E, 3), np.random.default_rng(T))
     w = synth.routing_weights(T, K, T + 1)
@@ -64,7 +68,7 @@ def test_full_size_layer_on_sampled_tokens(gpu, profile, T):
     tiled = {e: {k: (ops.tile_weights(v) if k.endswith("p") else v) for k, v in d.items()} for e, d in experts.items()}
     table = ops.expert_table(tiled, E, gpu, tiled=True)
     runner = ops.LayerRunner(gpu, E, D, I)
-    prof = PROFILE_BF16 if profile == "bf16" else PROFILE_A4W4
+    prof = {"bf16": PROFILE_BF16, "a4w4": PROFILE_A4W4, "bf16_pure": PROFILE_BF16_PURE}[profile]
     y = runner.forward(x.to(gpu), torch.from_numpy(ids).to(gpu), torch.from_numpy(w).to(gpu), table,
                        profile=prof, rule=RULE_OCP_FLOOR)
     torch.cuda.synchronize()
@@ -74,6 +78,8 @@ def test_full_size_layer_on_sampled_tokens(gpu, profile, T):
     host = {int(e): {k: v.cpu().numpy() for k, v in experts[int(e)].items()} for e in np.unique(ids[sample])}
     if profile == "bf16":
         ref = M.routed_bf16(xb[sample], ids[sample], w[sample], host, n_experts=E, workers=16)
+    elif profile == "bf16_pure":
+        ref = M.routed_bf16(xb[sample], ids[sample], w[sample], host, n_experts=E, workers=16, fp8_act=False)
     else:
         ref = M.routed_a4w4(xb[sample], ids[sample], w[sample], host, n_experts=E, rule="ocp_floor", workers=16)
     want = Q.bf16_bits_to_f32(ref["y"])

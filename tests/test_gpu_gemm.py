@@ -172,7 +172,8 @@ def test_layer_forward_vs_oracle(gpu, profile, T, K, E, D, I):
     # 16-row blocks up to 2047 routed rows (h quantised in the gate/up epilogue for a4w4,
     # by a separate launch for FP8); 256 tokens x top-8 = 2048 routed rows: 64-row M blocks
     # (tiled kernel, h quantised in the epilogue in both profiles); 3200 routed rows: the
-    # chunked two-launch align. The pure-bf16 variant runs 16-row blocks at every size.
+    # chunked two-launch align. The pure-bf16 variant takes the same block sizes (no h
+    # quantisation: its down GEMM reads bf16 h).
     ids, w, xb, host, devw, table = _case(T, K, E, D, I, 77 + T, gpu)
     runner = ops.LayerRunner(gpu, E, D, I)
     x = _dev_bf16(xb, gpu)
@@ -214,11 +215,15 @@ def test_layer_forward_ceil_rule_and_int32_ids(gpu):
 PURE_ACC_REL = 2.0 ** -16
 
 
-@pytest.mark.parametrize("T,K,E,D,I", [(24, 4, 16, 1024, 512), (8, 8, 256, 4096, 2048), (200, 8, 16, 512, 512)])
-def test_grouped_gemm_stages_bf16_pure(gpu, T, K, E, D, I):
+@pytest.mark.parametrize("block_m", [16, 64])
+@pytest.mark.parametrize("T,K,E,D,I", [(24, 4, 16, 1024, 512), (8, 8, 256, 4096, 2048), (200, 8, 16, 512, 512),
+                                       (300, 8, 8, 2048, 1024)])
+def test_grouped_gemm_stages_bf16_pure(gpu, T, K, E, D, I, block_m):
+    # 16-row blocks: the single-wave kernel; 64-row blocks: the LDS-tiled kernel
+    # (bf16 A tile in LDS, weight fragments dequantised once per 32-k half)
     from dsv4_hip import AFMT_BF16
     ids, w, xb, host, devw, table = _case(T, K, E, D, I, 71 + T, gpu)
-    al = ops.moe_align(_dev(ids, gpu), _dev(w, gpu), E, 16)
+    al = ops.moe_align(_dev(ids, gpu), _dev(w, gpu), E, block_m)
     R = T * K
     x = _dev_bf16(xb, gpu)
     h = ops.gemm_gateup(AFMT_BF16, x, None, K, al, table, D, I, _dev(w.reshape(-1), gpu), 10.0)
@@ -240,9 +245,9 @@ def test_grouped_gemm_stages_bf16_pure(gpu, T, K, E, D, I):
         h_ref[rows] = M.swiglu(g, u, w.reshape(-1)[rows], 10.0)
     h_gpu = Q.bf16_bits_to_f32(_bits(h))
     h_want = Q.f32_to_bf16_f32(h_ref)
-    print(f"pure bf16 gate/up T={T}: normwise rel {rel(h_gpu, h_want):.3e}")
+    print(f"pure bf16 gate/up T={T} block_m={block_m}: normwise rel {rel(h_gpu, h_want):.3e}")
     check_bound(h_gpu, h_want, swiglu_bound(g_all, u_all, w.reshape(-1), 10.0, h_want, g_abs, u_abs,
-                                            acc_rel=PURE_ACC_REL), f"pure bf16 gate/up T={T}")
+                                            acc_rel=PURE_ACC_REL), f"pure bf16 gate/up T={T} block_m={block_m}")
     # down on the oracle's bf16 h, as it is
     hb = Q.f32_to_bf16_bits(h_ref)
     out = ops.gemm_down(AFMT_BF16, _dev_bf16(hb, gpu), None, al, table, I, D)
@@ -256,11 +261,13 @@ def test_grouped_gemm_stages_bf16_pure(gpu, T, K, E, D, I):
         out_ref[rows] = M.matmul_nt(hf[rows], w2)
         out_abs[rows] = M.matmul_nt(np.abs(hf[rows]), np.abs(w2))
     out_gpu, out_want = Q.bf16_bits_to_f32(_bits(out)), Q.f32_to_bf16_f32(out_ref)
-    print(f"pure bf16 down T={T}: normwise rel {rel(out_gpu, out_want):.3e}")
-    check_bound(out_gpu, out_want, gemm_bound(out_want, out_abs, acc_rel=PURE_ACC_REL), f"pure bf16 down T={T}")
+    print(f"pure bf16 down T={T} block_m={block_m}: normwise rel {rel(out_gpu, out_want):.3e}")
+    check_bound(out_gpu, out_want, gemm_bound(out_want, out_abs, acc_rel=PURE_ACC_REL),
+                f"pure bf16 down T={T} block_m={block_m}")
 
 
-def test_dequant_in_the_bf16_gemm_every_byte_and_scale(gpu):
+@pytest.mark.parametrize("block_m", [16, 64])
+def test_dequant_in_the_bf16_gemm_every_byte_and_scale(gpu, block_m):
     # one-hot activations pick single weight elements: out[f][n] = W[n][k(f)] exactly, so
     # every packed byte value with every E8M0 byte 0..252 goes through the GEMM's
     # dequantisation and must equal the oracle's bf16 dequant (up to the sign of zero).
@@ -277,7 +284,7 @@ def test_dequant_in_the_bf16_gemm_every_byte_and_scale(gpu):
     table = ops.expert_table({0: ex}, E, gpu)
     R = I  # row f picks k = f
     ids = np.zeros((R, 1), np.int64)
-    al = ops.moe_align(_dev(ids, gpu), None, E, 16)
+    al = ops.moe_align(_dev(ids, gpu), None, E, block_m)
     one = np.zeros((R, I), np.float32)
     one[np.arange(R), np.arange(R)] = 1.0
     out = ops.gemm_down(AFMT_BF16, _dev_bf16(Q.f32_to_bf16_bits(one), gpu), None, al, table, I, D)

@@ -107,13 +107,16 @@ def test_npu_ops_align_permute_unpermute(gpu):
     assert np.array_equal(_bits(y), want)
 
 
+@pytest.mark.parametrize("counts", [[2, 0, 3], [1500, 0, 700]])
 @pytest.mark.parametrize("form", ["a4w4_list", "a4w4_stacked_view", "bf16_x", "bf16_x_pure"])
-def test_npu_ops_grouped_matmul_groups_2_0_3(gpu, form):
-    # _bench_gmm.py:8-22 group pattern, MXFP4 weights [N, K/2]
-    counts, N, Kd = [2, 0, 3], 256, 512
+def test_npu_ops_grouped_matmul_groups_2_0_3(gpu, form, counts):
+    # _bench_gmm.py:8-22 group pattern, MXFP4 weights [N, K/2]; 2200 rows take the
+    # 64-row blocks of the tiled kernel
+    N, Kd = 256, 512
+    M_rows = sum(counts)
     rng = np.random.default_rng(3)
     wts = [synth.packed_weight(rng, N, Kd) for _ in counts]
-    x = synth.bf16_normal(rng, (5, Kd))
+    x = synth.bf16_normal(rng, (M_rows, Kd))
     xb = x.view(torch.int16).numpy().view(np.uint16)
     if form == "bf16_x":
         rt = Q.act_quant(xb, 128)[0]
@@ -136,7 +139,7 @@ def test_npu_ops_grouped_matmul_groups_2_0_3(gpu, form):
             scale = [torch.stack([torch.from_numpy(s).reshape(N, Kd // 64, 2) for _, s in wts]).to(gpu)
                      .transpose(1, 2)]
         out = npu_ops.grouped_matmul(x=[torch.from_numpy(xp).to(gpu)], weight=weight, scale=scale,
-                                     per_token_scale=[torch.from_numpy(xs).to(gpu).reshape(5, Kd // 64, 2)],
+                                     per_token_scale=[torch.from_numpy(xs).to(gpu).reshape(M_rows, Kd // 64, 2)],
                                      group_list=torch.tensor(counts, device=gpu), group_list_type=1)
     got = Q.bf16_bits_to_f32(_bits(out))
     o = 0
