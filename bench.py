@@ -591,7 +591,7 @@ def main():
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(across GPUs the expert path would shard by expert, with an all-to-all of routed rows per layer)", file=sys.stderr)
         sys.exit(2)
-    from dsv4_hip import ops, PROFILE_A4W4, PROFILE_BF16, RULE_OCP_FLOOR
+    from dsv4_hip import ops, PROFILE_A4W4, PROFILE_BF16, PROFILE_BF16_PURE, RULE_OCP_FLOOR
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
@@ -604,6 +604,7 @@ def main():
         print(f"calib-copy: {src.numel()} bytes read, {dst.numel()} bytes written", file=sys.stderr)
         del src, dst
         torch.cuda.empty_cache()
+    pure_decode = None
     if args.only in ("", "decode"):
         pools, tables = gen_layer_weights(dev, args.layers, gen)
         host = routing_batches(64, T, K, 11)
@@ -612,6 +613,10 @@ def main():
         torch.cuda.synchronize()
         s = time_layer(runner, dev_b, tables, args.steps, args.warmup, PROFILE_BF16, RULE_OCP_FLOOR)
         gm = measure_gemms(dev_b, host, tables, min(args.steps, 100), PROFILE_BF16, RULE_OCP_FLOOR)
+        if not args.no_extra and args.only == "":  # the same layer without the FP8 round trips of x and h
+            sp = time_layer(runner, dev_b, tables, args.steps, args.warmup, PROFILE_BF16_PURE, RULE_OCP_FLOOR)
+            pure_decode = {"ms_per_layer": sp * 1e3, "tokens_per_s": T / sp,
+                           "vs_fp8_roundtrip_layer": s / sp}
         ach = gm["bytes_gateup"] / gm["t_gateup"] / 1e9
         # HBM bytes per launch from the committed counter profile (FETCH_SIZE/WRITE_SIZE
         # scaled by a 1 GiB copy): measured traffic / algorithmic bytes, applied to this run
@@ -644,6 +649,8 @@ def main():
     else:
         line = {"metric": "profile helper", "value": None}
     extra = {}
+    if pure_decode is not None:
+        extra["bf16_pure_decode_8"] = pure_decode
     if not args.no_extra and args.only in ("", "dequant"):
         extra["dequant_config0"] = measure_dequant(dev, gen)
         torch.cuda.empty_cache()
@@ -653,7 +660,7 @@ def main():
         legs = []
         if args.only in ("", "prefill", "prefill2048"):
             legs += [("a4w4_decode_64", 64, PROFILE_A4W4), ("bf16_prefill_2048", 2048, PROFILE_BF16),
-                     ("a4w4_prefill_2048", 2048, PROFILE_A4W4)]
+                     ("a4w4_prefill_2048", 2048, PROFILE_A4W4), ("bf16_pure_prefill_2048", 2048, PROFILE_BF16_PURE)]
         if args.only in ("", "prefill", "compute"):
             # the compute-bound point: 16384 tokens x top-8 = 131072 routed rows, every expert
             # with hundreds of rows, arithmetic intensity ~1.9 kFLOP/B (MXFP4 ridge ~1.26 kFLOP/B)
@@ -667,7 +674,8 @@ def main():
             A = float(np.mean([len(np.unique(b[1])) for b in host]))
             flops = 6.0 * Tn * K * D * I
             byts = A * EXPERT_BYTES + 4 * Tn * D
-            peak = MXFP4_PEAK_TFLOPS if prof == PROFILE_A4W4 else FP8_PEAK_TFLOPS
+            peak = {PROFILE_A4W4: MXFP4_PEAK_TFLOPS, PROFILE_BF16: FP8_PEAK_TFLOPS,
+                    PROFILE_BF16_PURE: BF16_PEAK_TFLOPS}[prof]
             extra[name] = {"ms_per_layer": s2 * 1e3, "tokens_per_s": Tn / s2, "tflops": flops / s2 / 1e12,
                            "frac_mfma_peak": flops / s2 / 1e12 / peak, "mfma_peak_tflops": peak,
                            "hbm_gbs": byts / s2 / 1e9, "frac_hbm": byts / s2 / 1e9 / HBM_PEAK_GBS,
