@@ -530,9 +530,10 @@ __global__ __launch_bounds__(64 * kWaves) void moe_gemm_kernel(Dsv4GemmArgs p) {
 // same XCD and re-read the weight tile from its L2.
 // ---------------------------------------------------------------------------
 // T0: first of the accumulator tiles this B stage feeds (E4M3 passes: 0, kNT/2)
+// live: bit mt set when row subtile mt holds a routed row (wave-uniform)
 template <int AFMT, int MT, bool B8 = false, int T0 = 0>
 DSV4_DEV void compute_tiled(v4f (*acc)[kNT], const uint8_t* lds, const uint8_t* as_tab, int as_pitch, int j,
-                            const BStageT<B8>& b, int r16, int g) {
+                            const BStageT<B8>& b, int r16, int g, uint32_t live) {
   constexpr int t0 = T0;
   constexpr int ASB = AFMT == 0 ? 256 : 128;
   constexpr int AROW = ASB + 16;
@@ -540,6 +541,7 @@ DSV4_DEV void compute_tiled(v4f (*acc)[kNT], const uint8_t* lds, const uint8_t* 
   for (int ji = 0; ji < 2; ++ji) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
+      if (!((live >> mt) & 1u)) continue;
       const int row = 16 * mt + r16;
       const uint8_t* ap = lds + row * AROW;
       v8i av;
@@ -591,10 +593,12 @@ DSV4_DEV void dequant_half(bf16x8_t (*bw)[4], const BStageT<false>& b, int ji) {
 }
 
 template <int MT>
-DSV4_DEV void mfma_half_bf16(v4f (*acc)[kNT], const uint8_t* lds, const bf16x8_t (*bw)[4], int ji, int r16, int g) {
+DSV4_DEV void mfma_half_bf16(v4f (*acc)[kNT], const uint8_t* lds, const bf16x8_t (*bw)[4], int ji, int r16, int g,
+                             uint32_t live) {
   constexpr int AROW = 512 + 16;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
+    if (!((live >> mt) & 1u)) continue;
     const uint8_t* ap = lds + (16 * mt + r16) * AROW + 64 * (2 * g + ji);
     v4i a[4];
 #pragma unroll
@@ -633,18 +637,32 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
   const bool have_w = GATEUP ? (ex.w1p && ex.w1s && ex.w3p && ex.w3s) : (ex.w2p && ex.w2s);
   const int r16 = lane & 15, g = lane >> 4;
 
+  // Row subtiles holding at least one routed row (bit mt of live). An expert's
+  // padding fills the end of its last block, so at 2048 tokens a third of the
+  // 64-row blocks' 16-row subtiles are padding only: their A chunks and MFMAs
+  // are skipped (wave-uniform branches; padding rows are never stored).
+  uint32_t live = 0;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const bool real = lane < 16 && p.sorted_ids[mb * BM + 16 * mt + lane] < p.R;
+    live |= (__ballot(real) != 0 ? 1u : 0u) << mt;
+  }
+
   // loader role: load v of wave w moves 1 KB of the stage's A tile = whole
   // 128-byte lines (4 rows x 256 B for E4M3, 8 rows x 128 B for E2M1), so each
-  // line is one L1->L2 request; lane L carries 16-byte chunk (v*NW + w)*64 + L
+  // line is one L1->L2 request; lane L carries 16-byte chunk (v*NW + w)*64 + L.
+  // The 64 chunks of one load lie in one row subtile (64 / CPRW rows, dividing 16).
   constexpr int CPRW = ASB / 16;  // 16-byte chunks per A row per stage
   const uint8_t* lsrc[LV];
   int ldst[LV];
+  bool lon[LV];
 #pragma unroll
   for (int v = 0; v < LV; ++v) {
     const int id = (v * NW + wave) * 64 + lane, row = id / CPRW, ch = id % CPRW;
     const int64_t ar = a_row<SH>(p, p.sorted_ids[mb * BM + row]);
     lsrc[v] = p.a + ar * p.a_row_bytes + 16 * ch;
     ldst[v] = row * AROW + 16 * ch;
+    lon[v] = (live >> (((v * NW + __builtin_amdgcn_readfirstlane(wave)) * 64 / CPRW) / 16)) & 1u;
   }
 
   const int64_t brow_bytes = shared ? p.Kdim : p.Kdim / 2, bsrow = p.Kdim / 32;
@@ -694,7 +712,8 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
     v4i lreg[LH];
     BStageT<false> b;
 #pragma unroll
-    for (int v = 0; v < LV; ++v) *(v4i*)&a_lds[0][ldst[v]] = ld16(lsrc[v]);
+    for (int v = 0; v < LV; ++v)
+      if (lon[v]) *(v4i*)&a_lds[0][ldst[v]] = ld16(lsrc[v]);
     load_b<false, false>(b, btp, bstp, 0, g, lay);
 #pragma unroll
     for (int t = 0; t < kNT; ++t) b.s[t] = ld_u16(bstp[t] + 2 * g);
@@ -705,7 +724,8 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
       uint8_t* nxt = a_lds[(j + 1) & 1];
       if (more) {
 #pragma unroll
-        for (int v = 0; v < LH; ++v) lreg[v] = ld16(lsrc[v] + (j + 1) * ASB);
+        for (int v = 0; v < LH; ++v)
+          if (lon[v]) lreg[v] = ld16(lsrc[v] + (j + 1) * ASB);
       }
       bf16x8_t bw[kNT][4];
 #pragma unroll
@@ -720,14 +740,16 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
           }
         }
         __builtin_amdgcn_sched_barrier(0);
-        mfma_half_bf16<MT>(acc, a_lds[j & 1], bw, ji, r16, g);
+        mfma_half_bf16<MT>(acc, a_lds[j & 1], bw, ji, r16, g, live);
         __builtin_amdgcn_sched_barrier(0);
         if (more) {
 #pragma unroll
-          for (int v = 0; v < LH; ++v) *(v4i*)&nxt[ldst[ji * LH + v]] = lreg[v];
+          for (int v = 0; v < LH; ++v)
+            if (lon[ji * LH + v]) *(v4i*)&nxt[ldst[ji * LH + v]] = lreg[v];
           if (ji == 0) {
 #pragma unroll
-            for (int v = 0; v < LH; ++v) lreg[v] = ld16(lsrc[LH + v] + (j + 1) * ASB);
+            for (int v = 0; v < LH; ++v)
+              if (lon[LH + v]) lreg[v] = ld16(lsrc[LH + v] + (j + 1) * ASB);
           }
         }
       }
@@ -753,7 +775,7 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
 #pragma unroll
     for (int i = 0; i < (AS_CHUNKS + NTH - 1) / NTH; ++i) {
       const int c = i * NTH + tid;
-      if (c < AS_CHUNKS) {
+      if (c < AS_CHUNKS && ((live >> (c / (KSB / 16) / 16)) & 1u)) {
         const int row = c / (KSB / 16), ch = c % (KSB / 16);
         const int64_t ar = a_row<SH>(p, p.sorted_ids[mb * BM + row]);
         *(v4i*)&as_tab[row * ASP + 16 * ch] = ld16(p.a_scale + ar * KSB + 16 * ch);
@@ -762,26 +784,30 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
     v4i lreg[LV];
     BStageT<B8> b[2];
 #pragma unroll
-    for (int v = 0; v < LV; ++v) lreg[v] = ld16(lsrc[v]);
+    for (int v = 0; v < LV; ++v)
+      if (lon[v]) lreg[v] = ld16(lsrc[v]);
     load_b<false, B8>(b[0], btp, bstp, 0, g, lay);
 #pragma unroll
-    for (int v = 0; v < LV; ++v) *(v4i*)&a_lds[0][ldst[v]] = lreg[v];
+    for (int v = 0; v < LV; ++v)
+      if (lon[v]) *(v4i*)&a_lds[0][ldst[v]] = lreg[v];
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < NST; ++j) {
       if (j + 1 < NST) {
 #pragma unroll
-        for (int v = 0; v < LV; ++v) lreg[v] = ld16(lsrc[v] + (j + 1) * ASB);
+        for (int v = 0; v < LV; ++v)
+          if (lon[v]) lreg[v] = ld16(lsrc[v] + (j + 1) * ASB);
         load_b<false, B8>(b[(j + 1) & 1], btp, bstp, j + 1, g, lay);
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int t = 0; t < NTB; ++t) b[j & 1].s[t] = stage_scales<NST>(bs_row[t], j, r16, g);
-      compute_tiled<AFMT, MT, B8, t0>(acc, a_lds[j & 1], as_tab, ASP, j, b[j & 1], r16, g);
+      compute_tiled<AFMT, MT, B8, t0>(acc, a_lds[j & 1], as_tab, ASP, j, b[j & 1], r16, g, live);
       __builtin_amdgcn_sched_barrier(0);
       if (j + 1 < NST) {
 #pragma unroll
-        for (int v = 0; v < LV; ++v) *(v4i*)&a_lds[(j + 1) & 1][ldst[v]] = lreg[v];
+        for (int v = 0; v < LV; ++v)
+          if (lon[v]) *(v4i*)&a_lds[(j + 1) & 1][ldst[v]] = lreg[v];
       }
       __syncthreads();
     }
