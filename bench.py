@@ -300,7 +300,7 @@ def measure_offload(dev, n_steps=512, n_layers=8, n_slots=512, T=8, K=8, warmup_
            "ms_per_layer": layer_s * 1e3, "layer_tokens_per_s": T / layer_s, "step_tokens_per_s": T / (wall / n_steps),
            "hit_rate": st["hits"] / max(lookups, 1), "misses_per_step": st["misses"] / n_steps,
            "h2d_gb": st["bytes_h2d"] / 1e9, "h2d_effective_gbs": st["bytes_h2d"] / wall / 1e9,
-           "evictions": st["evictions"]}
+           "hits": st["hits"], "misses": st["misses"], "evictions": st["evictions"], "warmup_steps": warmup_steps}
     if prefetch_steps > 0:
         cache.reset_stats()
         t0 = time.perf_counter()
@@ -508,6 +508,26 @@ def _timed(fn, min_seconds, min_runs=1, warmup=True):
     return (time.perf_counter() - t0) / n, n
 
 
+def offload_lru_replay(res, n_layers=8, n_slots=512, T=8, K=8):
+    """The offload leg's acquisitions (its warm-up steps, then the timed steps) replayed
+    through the textbook LRU the reference's ExpertBank implements (offload.py:103-129);
+    the slot cache's hit, miss and eviction counts over the timed steps must equal it."""
+    from oracle.lru import LRUOracle
+    from dsv4_hip import synth
+    route = synth.DriftingZipf(n_layers, E, K)
+    lru = LRUOracle(n_slots)
+    for s in range(res["warmup_steps"] + res["steps"]):
+        if s == res["warmup_steps"]:
+            lru.hits = lru.misses = lru.evictions = 0
+        for l, ids in enumerate(route.step(T)):
+            for e in np.unique(ids):
+                lru.access((l, int(e)))
+    got = (res["hits"], res["misses"], res["evictions"])
+    want = (lru.hits, lru.misses, lru.evictions)
+    assert got == want, f"offload slot cache (hits, misses, evictions) {got} != LRU replay {want}"
+    return {"hits": lru.hits, "misses": lru.misses, "evictions": lru.evictions, "matches_slot_cache": True}
+
+
 def cpu_baselines(threads=None, seconds=8.0):
     """The numpy oracle of configs 0, 2, 3 and 4 on the host cores (reported baselines;
     config 1 is ``cpu_baseline``). Each is a bounded sample: a few calls after one
@@ -700,6 +720,8 @@ def main():
         line["cpu_baseline"]["host_threads_available"] = os.cpu_count()
     if not args.no_cpu_baseline and args.only in ("", "cpu"):
         extra["cpu_baselines"] = cpu_baselines()
+        if "offload_config4" in extra:  # the CPU leg checks the offload leg's policy too
+            extra["offload_config4"]["lru_replay"] = offload_lru_replay(extra["offload_config4"])
         line["extra"] = extra
     print(json.dumps(line), flush=True)
 
