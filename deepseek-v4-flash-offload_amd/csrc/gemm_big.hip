@@ -2,23 +2,26 @@
 //
 // moe_align gives every expert with at least `hot_min` routed rows its own
 // layout of 256-row M blocks (the "hot" layout); this kernel runs those
-// blocks. One workgroup = 4 waves = 256 rows x 256 weight rows (gate/up: 128
+// blocks. One workgroup = 8 waves = 256 rows x 256 weight rows (gate/up: 128
 // gate + the 128 matching up rows; down: 256 output rows of W2). Both operand
 // tiles of each 64-k stage go through LDS - the A rows gathered through
 // sorted_ids, the weight rows from the expert's slot - so every weight byte a
 // block brings from L2 serves 256 rows (the 16/64-row kernels re-read an
 // expert's weights once per 16 or 64 rows) and every A byte 256 weight rows.
-// Each wave (one per SIMD) owns 128 rows x 128 weight rows: 4 x 4 tiles of
-// v_mfma_scale_f32_32x32x64_f8f6f4 whose 256 accumulator registers live in
-// the AGPRs, so every fragment read from LDS feeds four MFMAs. The 32x32x64
-// form carries twice the FLOPs per operand byte of the 16x16x128 one (and ran
-// fp4 x fp4 at 7.25 PFLOP/s against 6.7 in an MFMA-loop probe on this part).
+// Each wave (two per SIMD) owns 128 rows x 64 weight rows: 4 x 2 tiles of
+// v_mfma_scale_f32_32x32x64_f8f6f4 (128 accumulator registers), so each weight
+// fragment read from LDS feeds four MFMAs and each activation fragment two. Two
+// waves per SIMD let one wave's MFMAs run while the other waits at a barrier or
+// on its LDS reads: against one 128 x 128 wave per SIMD (256 accumulators in
+// the AGPRs) the kernels took 4-8 % less time. The 32x32x64 form carries twice
+// the FLOPs per operand byte of the 16x16x128 one (and ran fp4 x fp4 at 7.25
+// PFLOP/s against 6.7 in an MFMA-loop probe on this part).
 //
 // Operands move global -> LDS with global_load_lds_dwordx4 (lane i of one
 // instruction writes its 16 bytes at the instruction's LDS base + 16 i): no
 // staging registers, so a ring of NB stage slots keeps NB - 1 stages of loads
 // in flight (96 KB per CU with FP8 A). With one workgroup per CU there are no
-// other waves to hide the load latency behind; the depth of the ring does.
+// other workgroups to hide the load latency behind; the depth of the ring does.
 // Each 1-KB chunk is laid out in the order the MFMA lanes read it, with an XOR
 // swizzle that puts the 16 lanes of each ds_read_b128 pass on distinct banks.
 //
@@ -52,7 +55,8 @@ typedef __attribute__((address_space(3))) void lvoid;
 
 constexpr int kBM = 256;     // rows per block
 constexpr int kBN = 256;     // weight rows per block
-constexpr int kNT = 256;     // threads (4 waves, one per SIMD)
+constexpr int kNT = 512;     // threads (8 waves, two per SIMD)
+constexpr int kWT = 2;       // 32-row weight tiles per wave
 constexpr int kKS = 64;      // k per stage
 constexpr int kSS = 16;      // stages per scale super-stage (1024 k)
 
@@ -62,8 +66,8 @@ struct Big {
   static constexpr int BCH = kBN * (kKS / 2) / 1024;  // 1-KB weight chunks per stage
   static constexpr int STAGE = (ACH + BCH) * 1024;
   static constexpr int NB = AFMT == 0 ? 5 : 7;       // stage slots of the ring
-  static constexpr int AV = ACH / 4;                  // A loads per thread per stage
-  static constexpr int BV = BCH / 4;                  // weight loads per thread per stage
+  static constexpr int AV = ACH / 8;                  // A loads per thread per stage
+  static constexpr int BV = BCH / 8;                  // weight loads per thread per stage
   static constexpr int L = AV + BV;
   // scales: one super-stage = 32 bytes per A row and per weight row (two 16-byte
   // pieces), loaded by LDS-DMA once per 16 stages into one of two buffers; a buffer
@@ -143,10 +147,10 @@ DSV4_DEV void big_dma_stage(uint8_t* slot, const uint8_t* const* a_src, const ui
 // A tiles mt (E4M3: 2 x 16 bytes, E2M1: 16 bytes; + scale each).
 template <int AFMT>
 struct BigFrag {
-  v4i b[4];
+  v4i b[kWT];
   v4i lo[4];
   v4i hi[AFMT == 0 ? 4 : 1];
-  int sb[4], sa[4];
+  int sb[kWT], sa[4];
 };
 
 // Reads one stage's fragments from ring slot L. S: the scale super-stage buffer, q0:
@@ -157,7 +161,7 @@ DSV4_DEV void big_read(BigFrag<AFMT>& F, const uint8_t* L, const uint8_t* S, int
                        int r32, int g2, int a_lo, int a_hi, int b_lane) {
   using C = Big<AFMT>;
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) {
+  for (int nt = 0; nt < kWT; ++nt) {
     F.b[nt] = *(const v4i*)(L + (C::ACH + brow0[nt] / 32) * 1024 + b_lane);
     F.sb[nt] = scale_byte<true>(S, brow0[nt] + r32, q0 + g2);
   }
@@ -181,9 +185,9 @@ DSV4_DEV void big_read(BigFrag<AFMT>& F, const uint8_t* L, const uint8_t* S, int
 // the reads are done long before the next barrier waits for them.
 template <int AFMT>
 DSV4_DEV void big_sched() {
-  constexpr int kReads = AFMT == 0 ? 20 : 16;  // ds_reads of big_read
+  constexpr int kReads = AFMT == 0 ? 16 : 12;  // ds_reads of big_read
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < 4 * kWT; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA
     if (i < Big<AFMT>::L) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
     if (2 * i < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);    // DS read
@@ -195,14 +199,14 @@ DSV4_DEV void big_sched() {
 // columns x tokens: register r of lane l = weight column 8(r/4) + 4(l/32) + r%4 of
 // weight tile wt, token l%32 of token tile tt (the E4M3 B layout is the A layout).
 template <int AFMT>
-DSV4_DEV void big_mfma(v16f (&acc)[4][4], const BigFrag<AFMT>& F) {
+DSV4_DEV void big_mfma(v16f (&acc)[4][kWT], const BigFrag<AFMT>& F) {
 #pragma unroll
   for (int tt = 0; tt < 4; ++tt) {
     const v4i lo = F.lo[tt];
     const v4i hi = AFMT == 0 ? F.hi[tt] : v4i{0, 0, 0, 0};
     const v8i xf = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
-    for (int wt = 0; wt < 4; ++wt) {
+    for (int wt = 0; wt < kWT; ++wt) {
       const v8i wf = v8i{F.b[wt].x, F.b[wt].y, F.b[wt].z, F.b[wt].w, 0, 0, 0, 0};
       acc[tt][wt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf, xf, acc[tt][wt], 4, AFMT == 0 ? 0 : 4, 0,
                                                                    F.sb[wt], 0, F.sa[tt]);
@@ -214,7 +218,7 @@ DSV4_DEV void big_mfma(v16f (&acc)[4][4], const BigFrag<AFMT>& F) {
 // Each lane holds, per token tile tt, 4-column runs of one token's row (columns
 // 8q + 4(l/32) + e of every 32-column weight tile): SwiGLU, the quantisation blocks'
 // maxima (in-lane, then across the lane pair l, l ^ 32, then - FP8 h only - across the
-// two waves of a token row through the LDS) and the packing all stay in registers.
+// four waves of a token row through the LDS) and the packing all stay in registers.
 // bf16 / E4M3 / E2M1 conversions use the gfx950 converters, which agree bit for bit
 // with the library's software quantisers on every input they see here (RNE; E4M3 after
 // the clamp to +-448; E2M1 with the sign of the input, whose -0 the rule-0 path
@@ -291,7 +295,7 @@ __global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
   using C = Big<AFMT>;
   __shared__ __attribute__((aligned(16))) uint8_t lds[C::LDS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
   int mb, nt;
   big_tile_of_block(mb, nt);
   if (mb * kBM >= p.num_post_padded[0]) return;  // also every block of the grid's padding
@@ -345,11 +349,11 @@ __global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
     }
   }
 
-  v16f acc[4][4];
+  v16f acc[4][kWT];
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = v16f{};
+    for (int nt = 0; nt < kWT; ++nt) acc[mt][nt] = v16f{};
   const int r32 = lane & 31, g2 = lane >> 5;
   // flat index (and gate/up: routing weight) of this lane's token in each token tile
   int fr[4];
@@ -360,9 +364,11 @@ __global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
     wr[tt] = GATEUP && fr[tt] < p.R ? p.topk_w[fr[tt]] : 0.0f;
   }
   // first weight row of this wave's 32-row tile nt in the block
-  int brow0[4];
+  // gate/up: tile 0 = gate rows 32 wn.., tile 1 = the matching up rows 128 + 32 wn..;
+  // down: output rows 64 wn + 32 nt..
+  int brow0[kWT];
 #pragma unroll
-  for (int nt = 0; nt < 4; ++nt) brow0[nt] = GATEUP ? (nt >> 1) * 128 + 64 * wn + 32 * (nt & 1) : 128 * wn + 32 * nt;
+  for (int nt = 0; nt < kWT; ++nt) brow0[nt] = GATEUP ? nt * 128 + 32 * wn : 64 * wn + 32 * nt;
   // this lane's byte offsets inside a chunk (the swizzles of the layout comment)
   int a_lo, a_hi;
   if (AFMT == 0) {
@@ -428,28 +434,26 @@ __global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
 
   // epilogue (every wave is past the ring: the LDS is free)
   if (GATEUP) {
-    const int cw = c0 + 64 * wn;  // this wave's first intermediate column
-    // h for columns cw + 32 h2 + 8 q + 4 g2 + e of token tile tt, packed bf16 pairs
-    uint32_t hp[4][2][4][2];
+    const int cw = c0 + 32 * wn;  // this wave's 32 intermediate columns
+    // h for columns cw + 8 q + 4 g2 + e of token tile tt, packed bf16 pairs
+    uint32_t hp[4][4][2];
     float rmax[4];
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
       float m = 0.0f;
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2)
+      for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int e = 0; e < 4; e += 2) {
-            const int r = 4 * q + e;
-            // gate (tile h2) and up (tile h2 + 2) of the same column, rounded to bf16
-            const uint32_t gu0 = pk_bf16(acc[tt][h2][r], acc[tt][h2 + 2][r]);
-            const uint32_t gu1 = pk_bf16(acc[tt][h2][r + 1], acc[tt][h2 + 2][r + 1]);
-            const uint32_t hw = pk_bf16(big_swiglu(bf16_lo(gu0), bf16_hi(gu0), wr[tt], p.swiglu_limit),
-                                        big_swiglu(bf16_lo(gu1), bf16_hi(gu1), wr[tt], p.swiglu_limit));
-            hp[tt][h2][q][e >> 1] = hw;
-            m = fmaxf(m, fmaxf(fabsf(bf16_lo(hw)), fabsf(bf16_hi(hw))));
-          }
+        for (int e = 0; e < 4; e += 2) {
+          const int r = 4 * q + e;
+          // gate (tile 0) and up (tile 1) of the same column, rounded to bf16
+          const uint32_t gu0 = pk_bf16(acc[tt][0][r], acc[tt][1][r]);
+          const uint32_t gu1 = pk_bf16(acc[tt][0][r + 1], acc[tt][1][r + 1]);
+          const uint32_t hw = pk_bf16(big_swiglu(bf16_lo(gu0), bf16_hi(gu0), wr[tt], p.swiglu_limit),
+                                      big_swiglu(bf16_lo(gu1), bf16_hi(gu1), wr[tt], p.swiglu_limit));
+          hp[tt][q][e >> 1] = hw;
+          m = fmaxf(m, fmaxf(fabsf(bf16_lo(hw)), fabsf(bf16_hi(hw))));
+        }
       rmax[tt] = m;
     }
     if (!p.hq_skip_h && p.out) {
@@ -457,43 +461,29 @@ __global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
       for (int tt = 0; tt < 4; ++tt)
         if (fr[tt] < p.R)
 #pragma unroll
-          for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              typedef uint32_t v2u __attribute__((ext_vector_type(2)));
-              *(v2u*)(p.out + (int64_t)fr[tt] * p.N + cw + 32 * h2 + 8 * q + 4 * g2) =
-                  v2u{hp[tt][h2][q][0], hp[tt][h2][q][1]};
-            }
-    }
-    if (p.hq_mode == 2) {  // MXFP4 h: one 32-column block per (tt, h2), half of it in each lane of a pair
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-        for (int h2 = 0; h2 < 2; ++h2) {
-          float m = 0.0f;
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-              const uint32_t w = hp[tt][h2][q][j];
-              m = fmaxf(m, fmaxf(fabsf(bf16_lo(w)), fabsf(bf16_hi(w))));
-            }
-          const int k = dsv4::mxfp4_block_exp(max_pair(m), p.hq_rule);
-          const float inv = dsv4::pow2f(-k);
-          if (fr[tt] < p.R) {
-            const int col = cw + 32 * h2;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const uint32_t w0 = hp[tt][h2][q][0], w1 = hp[tt][h2][q][1];
-              const uint32_t nib = pk_fp4x2(bf16_lo(w0), bf16_hi(w0), inv, p.hq_rule) |
-                                   pk_fp4x2(bf16_lo(w1), bf16_hi(w1), inv, p.hq_rule) << 8;
-              *(uint16_t*)(p.hq_codes + (int64_t)fr[tt] * (p.N / 2) + (col + 8 * q + 4 * g2) / 2) = (uint16_t)nib;
-            }
-            if (g2 == 0) p.hq_scale[(int64_t)fr[tt] * (p.N / 32) + col / 32] = (uint8_t)(k + 127);
+          for (int q = 0; q < 4; ++q) {
+            typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+            *(v2u*)(p.out + (int64_t)fr[tt] * p.N + cw + 8 * q + 4 * g2) = v2u{hp[tt][q][0], hp[tt][q][1]};
           }
+    }
+    if (p.hq_mode == 2) {  // MXFP4 h: one 32-column block per token tile, half of it in each lane of a pair
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const int k = dsv4::mxfp4_block_exp(max_pair(rmax[tt]), p.hq_rule);
+        const float inv = dsv4::pow2f(-k);
+        if (fr[tt] < p.R) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t w0 = hp[tt][q][0], w1 = hp[tt][q][1];
+            const uint32_t nib = pk_fp4x2(bf16_lo(w0), bf16_hi(w0), inv, p.hq_rule) |
+                                 pk_fp4x2(bf16_lo(w1), bf16_hi(w1), inv, p.hq_rule) << 8;
+            *(uint16_t*)(p.hq_codes + (int64_t)fr[tt] * (p.N / 2) + (cw + 8 * q + 4 * g2) / 2) = (uint16_t)nib;
+          }
+          if (g2 == 0) p.hq_scale[(int64_t)fr[tt] * (p.N / 32) + cw / 32] = (uint8_t)(k + 127);
         }
-    } else if (p.hq_mode == 1) {  // FP8 h: one 128-column block per token, split over the wn pair of waves
-      float* am = (float*)lds;     // [2 wn][256 rows]
+      }
+    } else if (p.hq_mode == 1) {  // FP8 h: one 128-column block per token, split over the four wn waves
+      float* am = (float*)lds;     // [4 wn][256 rows]
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         rmax[tt] = max_pair(rmax[tt]);
@@ -502,28 +492,28 @@ __global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
       __syncthreads();
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
-        const int k = dsv4::fp8_block_exp(fmaxf(rmax[tt], am[(1 - wn) * 256 + 128 * wm + 32 * tt + r32]));
+        const int row = 128 * wm + 32 * tt + r32;
+        const float bm = fmaxf(fmaxf(am[row], am[256 + row]), fmaxf(am[512 + row], am[768 + row]));
+        const int k = dsv4::fp8_block_exp(bm);
         const float inv = dsv4::pow2f(-k);
         if (fr[tt] < p.R) {
 #pragma unroll
-          for (int h2 = 0; h2 < 2; ++h2)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const uint32_t w0 = hp[tt][h2][q][0], w1 = hp[tt][h2][q][1];
-              *(uint32_t*)(p.hq_codes + (int64_t)fr[tt] * p.N + cw + 32 * h2 + 8 * q + 4 * g2) =
-                  pk_fp8x4(bf16_lo(w0), bf16_hi(w0), bf16_lo(w1), bf16_hi(w1), inv);
-            }
-          if (g2 == 0) *(uint16_t*)(p.hq_scale + (int64_t)fr[tt] * (p.N / 32) + cw / 32) = (uint16_t)((k + 127) * 0x0101);
+          for (int q = 0; q < 4; ++q) {
+            const uint32_t w0 = hp[tt][q][0], w1 = hp[tt][q][1];
+            *(uint32_t*)(p.hq_codes + (int64_t)fr[tt] * p.N + cw + 8 * q + 4 * g2) =
+                pk_fp8x4(bf16_lo(w0), bf16_hi(w0), bf16_lo(w1), bf16_hi(w1), inv);
+          }
+          if (g2 == 0) p.hq_scale[(int64_t)fr[tt] * (p.N / 32) + cw / 32] = (uint8_t)(k + 127);
         }
       }
     }
   } else {
-    const int cw = c0 + 128 * wn;  // this wave's first output column
+    const int cw = c0 + 64 * wn;  // this wave's first output column
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt)
       if (fr[tt] < p.R)
 #pragma unroll
-        for (int wt = 0; wt < 4; ++wt)
+        for (int wt = 0; wt < kWT; ++wt)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             typedef uint32_t v2u __attribute__((ext_vector_type(2)));
