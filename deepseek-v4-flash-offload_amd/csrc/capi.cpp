@@ -382,28 +382,28 @@ struct LayerWs {
   int64_t sorted_ids_h, block_expert_h, npp_h;
 };
 
-// Experts with at least this many routed rows run in 256-row blocks on the
-// large-tile kernel in layers of at least kHotLayerRows routed rows; the rest keep
-// 64-row blocks. DSV4_HOT_ROWS overrides it (0: never), read once.
-// Below this many routed rows (8192 tokens at top-8) the hot experts' blocks are too
-// few to fill a launch of their own: measured with Zipf(1.1) routing over 256 experts
-// (hidden 4096, inter 2048), the two-launch split lost 2-10% at 2048-6144 tokens and
-// gained 2% at 8192, 5% at 12288 and 7-10% at 16384.
-// DSV4_HOT_LAYER_ROWS overrides it, read once.
+// Experts with at least hot_rows_threshold(R) routed rows run in 256-row blocks on
+// the large-tile kernel in layers of at least hot_layer_rows() routed rows; the rest
+// keep 64-row blocks. Measured with Zipf(1.1) routing over 256 experts (hidden 4096,
+// inter 2048) and the eight-wave large-tile kernel: the two-launch split lost 10 % at
+// 2048 tokens (the hot experts' blocks too few to fill a launch of their own) and
+// gained 2 % (bf16) / 5.5 % (a4w4) at 4096 tokens with a 256-row threshold; from 8192
+// tokens a 128-row threshold was 2-3 % faster than 256 (which the 4096-token layer
+// preferred). DSV4_HOT_LAYER_ROWS and DSV4_HOT_ROWS (0: never) override them, read once.
 static int64_t hot_layer_rows() {
   static const int64_t v = [] {
     const char* s = getenv("DSV4_HOT_LAYER_ROWS");
-    return s ? (int64_t)atoll(s) : (int64_t)65536;
+    return s ? (int64_t)atoll(s) : (int64_t)32768;
   }();
   return v;
 }
 
-static int hot_rows_threshold() {
+static int hot_rows_threshold(int64_t R) {
   static const int v = [] {
     const char* s = getenv("DSV4_HOT_ROWS");
-    return s ? atoi(s) : 256;
+    return s ? atoi(s) : -1;
   }();
-  return v;
+  return v >= 0 ? v : (R >= 65536 ? 128 : 256);
 }
 
 // Rows per M block: 16 (decode kernel, ~1-4 rows per active expert) below 2048
@@ -438,7 +438,7 @@ static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool sha
   w.out = take(2 * Rt * D);
   w.align_scratch = R > kAlignSmallRows ? take(align_chunked_scratch_bytes((int)R, E)) : 0;
   w.route_part = routed ? take(dsv4_moe_route_workspace_bytes(T, D, E)) : -1;  // router partial logits
-  const int hot = hot_rows_threshold();
+  const int hot = hot_rows_threshold(R);
   if (!pure && R >= hot_layer_rows() && R > kAlignSmallRows && hot > 0 && moe_gemm_big_supported(D, I, true) &&
       moe_gemm_big_supported(I, D, false)) {
     w.hot_min = hot;

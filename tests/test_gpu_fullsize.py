@@ -57,8 +57,8 @@ def _device_experts(dev, seed):
     return ex
 
 
-@pytest.mark.parametrize("profile,T", [("bf16", 2048), ("a4w4", 2048), ("a4w4", 64), ("bf16", 16384),
-                                       ("a4w4", 16384), ("bf16_pure", 2048)])
+@pytest.mark.parametrize("profile,T", [("bf16", 2048), ("a4w4", 2048), ("a4w4", 64), ("bf16", 4096),
+                                       ("a4w4", 4096), ("bf16", 16384), ("a4w4", 16384), ("bf16_pure", 2048)])
 def test_full_size_layer_on_sampled_tokens(gpu, profile, T):
     ids = synth.zipf_topk(T, K, E, synth.rank_permutation(E, 3), np.random.default_rng(T))
     w = synth.routing_weights(T, K, T + 1)
@@ -98,20 +98,22 @@ def test_full_size_layer_on_sampled_tokens(gpu, profile, T):
 def _sample_tokens(ids, T, n_hot=16, n_random=32):
     """Tokens of the first and last routed row of every M block of the n_hot
     hottest experts (rows of an expert in flat-index order, blocks of the
-    layer's block size: 64 rows from 2048 routed rows on, else 16; 256 for
-    experts with at least 256 rows from 65,536 routed rows on, where only the
-    8 hottest are taken), plus n_random random tokens; every token when T <= 64."""
+    layer's block size: 64 rows from 2048 routed rows on, else 16; 256 for the
+    experts the large-tile split takes - at least 256 rows from 32,768 routed
+    rows on, at least 128 from 65,536 - where only the 8 hottest are taken),
+    plus n_random random tokens; every token when T <= 64."""
     if T <= 64:
         return np.arange(T)
     R = ids.size
     flat = ids.reshape(-1)
     counts = np.bincount(flat, minlength=E)
     picks = set()
-    if R >= 65536:  # the layer's large-tile split: 256-row blocks for experts with >= 256 rows
+    hot_min = 128 if R >= 65536 else 256  # the layer's large-tile split (256-row blocks)
+    if R >= 32768:
         n_hot = 8
     for e in np.argsort(-counts, kind="stable")[:n_hot]:
         tok = np.nonzero(flat == e)[0] // ids.shape[1]
-        bm = 256 if (R >= 65536 and tok.size >= 256) else (64 if R >= 2048 else 16)
+        bm = 256 if (R >= 32768 and tok.size >= hot_min) else (64 if R >= 2048 else 16)
         for b in range(0, tok.size, bm):
             picks.add(int(tok[b]))
             picks.add(int(tok[min(b + bm, tok.size) - 1]))
