@@ -2,26 +2,30 @@
 //
 // moe_align gives every expert with at least `hot_min` routed rows its own
 // layout of 256-row M blocks (the "hot" layout); this kernel runs those
-// blocks. One workgroup = 8 waves = 256 rows x 256 weight rows (gate/up: 128
-// gate + the 128 matching up rows; down: 256 output rows of W2). Both operand
-// tiles of each 64-k stage go through LDS - the A rows gathered through
-// sorted_ids, the weight rows from the expert's slot - so every weight byte a
-// block brings from L2 serves 256 rows (the 16/64-row kernels re-read an
-// expert's weights once per 16 or 64 rows) and every A byte 256 weight rows.
-// Each wave (two per SIMD) owns 128 rows x 64 weight rows: 4 x 2 tiles of
-// v_mfma_scale_f32_32x32x64_f8f6f4 (128 accumulator registers), so each weight
-// fragment read from LDS feeds four MFMAs and each activation fragment two. Two
-// waves per SIMD let one wave's MFMAs run while the other waits at a barrier or
-// on its LDS reads: against one 128 x 128 wave per SIMD (256 accumulators in
-// the AGPRs) the kernels took 4-8 % less time. The 32x32x64 form carries twice
-// the FLOPs per operand byte of the 16x16x128 one (and ran fp4 x fp4 at 7.25
-// PFLOP/s against 6.7 in an MFMA-loop probe on this part).
+// blocks against 256 weight rows (gate/up: 128 gate + the 128 matching up rows;
+// down: 256 output rows of W2). Both operand tiles of each 64-k stage go through
+// LDS - the A rows gathered through sorted_ids, the weight rows from the
+// expert's slot - so every weight byte a workgroup brings from L2 serves 128 or
+// 256 rows (the 16/64-row kernels re-read an expert's weights once per 16 or 64
+// rows) and every A byte 256 weight rows. Two waves share each SIMD, each with
+// 128 accumulator registers of v_mfma_scale_f32_32x32x64_f8f6f4 tiles:
+//   E2M1 A (a4w4)  : one workgroup of 8 waves per CU over the whole 256-row block;
+//                    a wave owns 128 rows x 64 weight rows (4 x 2 tiles).
+//   E4M3 A (bf16)  : two workgroups of 4 waves per CU, each over half a block
+//                    (128 rows); a wave owns 64 rows x 128 weight rows (2 x 4).
+// A weight fragment read from LDS feeds TT MFMAs and an activation fragment WT.
+// Two waves per SIMD let one wave's MFMAs run while the other waits at a barrier
+// or on its LDS reads (against one 128 x 128 wave per SIMD, 256 accumulators in
+// the AGPRs, the kernels took 4-8 % less time); two independent workgroups per CU
+// also keep the MFMAs of one busy while the other crosses its stage barrier. The
+// 32x32x64 form carries twice the FLOPs per operand byte of the 16x16x128 one (and
+// ran fp4 x fp4 at 7.25 PFLOP/s against 6.7 in an MFMA-loop probe on this part).
 //
 // Operands move global -> LDS with global_load_lds_dwordx4 (lane i of one
 // instruction writes its 16 bytes at the instruction's LDS base + 16 i): no
 // staging registers, so a ring of NB stage slots keeps NB - 1 stages of loads
-// in flight (96 KB per CU with FP8 A). With one workgroup per CU there are no
-// other workgroups to hide the load latency behind; the depth of the ring does.
+// in flight (96 KB per CU with E2M1 A and one workgroup, 2 x 48 KB with E4M3 A);
+// the depth of the ring, and the second workgroup, hide the load latency.
 // Each 1-KB chunk is laid out in the order the MFMA lanes read it, with an XOR
 // swizzle that puts the 16 lanes of each ds_read_b128 pass on distinct banks.
 //
@@ -53,21 +57,40 @@ typedef __attribute__((address_space(1))) const v4i gv4i;
 typedef __attribute__((address_space(1))) const void gvoid;
 typedef __attribute__((address_space(3))) void lvoid;
 
-constexpr int kBM = 256;     // rows per block
+constexpr int kHB = 256;     // rows per block of the hot layout
 constexpr int kBN = 256;     // weight rows per block
-constexpr int kNT = 512;     // threads (8 waves, two per SIMD)
-constexpr int kWT = 2;       // 32-row weight tiles per wave
 constexpr int kKS = 64;      // k per stage
 constexpr int kSS = 16;      // stages per scale super-stage (1024 k)
 
+// Workgroup shape per activation format. E4M3 (bf16 profile): two workgroups per CU,
+// each half a 256-row block, 4 waves of 64 rows x 128 weight rows; E2M1 (a4w4): one
+// workgroup per CU over the whole block, 8 waves of 128 x 64. Either way two waves share
+// a SIMD; two independent workgroups let one's MFMAs run while the other waits at its
+// stage barrier. Measured at 16384 tokens (layer time, same runs): E4M3 4.49-4.60 ms with
+// the 8-wave shape against 4.27-4.29 with the half-block one; E2M1 3.66-3.68 with the
+// 8-wave shape against 3.73-3.76.
+template <int AFMT>
+struct Cfg {
+  static constexpr bool HALF = AFMT == 0;
+  static constexpr int BM = HALF ? 128 : 256;  // rows per workgroup
+  static constexpr int NT = HALF ? 256 : 512;  // threads
+  static constexpr int NW = NT / 64;           // waves
+  static constexpr int WM = 2, WN = NW / WM;   // wave grid over rows x weight rows
+  static constexpr int TT = BM / WM / 32;      // 32-row token tiles per wave
+  static constexpr int WT = kBN / WN / 32;     // 32-row weight tiles per wave
+  static constexpr int WGS = HALF ? 2 : 1;     // workgroups per CU
+};
+
 template <int AFMT>
 struct Big {
-  static constexpr int ACH = AFMT == 0 ? 16 : 8;     // 1-KB A chunks per stage
+  static constexpr int kBM = Cfg<AFMT>::BM;
+  static constexpr int kNT = Cfg<AFMT>::NT;
+  static constexpr int ACH = kBM * (AFMT == 0 ? kKS : kKS / 2) / 1024;  // 1-KB A chunks per stage
   static constexpr int BCH = kBN * (kKS / 2) / 1024;  // 1-KB weight chunks per stage
   static constexpr int STAGE = (ACH + BCH) * 1024;
-  static constexpr int NB = AFMT == 0 ? 5 : 7;       // stage slots of the ring
-  static constexpr int AV = ACH / 8;                  // A loads per thread per stage
-  static constexpr int BV = BCH / 8;                  // weight loads per thread per stage
+  static constexpr int NB = AFMT == 0 ? 3 : 7;        // stage slots of the ring
+  static constexpr int AV = ACH / Cfg<AFMT>::NW;      // A loads per thread per stage
+  static constexpr int BV = BCH / Cfg<AFMT>::NW;      // weight loads per thread per stage
   static constexpr int L = AV + BV;
   // scales: one super-stage = 32 bytes per A row and per weight row (two 16-byte
   // pieces), loaded by LDS-DMA once per 16 stages into one of two buffers; a buffer
@@ -78,7 +101,7 @@ struct Big {
   static constexpr int BS_OFF = kBM * 32;            // weight rows within a buffer
   static constexpr int SV = SCL / (kNT * 16);         // scale loads per thread per super-stage
   static constexpr int LDS = NB * STAGE + 2 * SCL;
-  static_assert(LDS <= 160 * 1024, "the stage ring and two scale super-stages must fit the LDS");
+  static_assert(LDS * Cfg<AFMT>::WGS <= 160 * 1024, "the stage ring and two scale super-stages must fit the LDS");
   static_assert(BCH == 8 && (ACH * 1024) == kBM * (AFMT == 0 ? kKS : kKS / 2), "chunking");
 };
 
@@ -122,8 +145,9 @@ DSV4_DEV void big_dma_scales(uint8_t* lds, int buf, const uint8_t* const* sc_src
 
 // The E8M0 byte q (0..31, the 32-k block within the super-stage) of row `row` of the
 // A (B = false) or weight (B = true) rows in scale buffer S.
-template <bool B>
+template <int AFMT, bool B>
 DSV4_DEV int scale_byte(const uint8_t* S, int row, int q) {
+  constexpr int kBM = Cfg<AFMT>::BM;
   return S[(B ? kBM * 32 : 0) + ((q >> 4) * (B ? kBN : kBM) + row) * 16 + (q & 15)];
 }
 
@@ -147,10 +171,10 @@ DSV4_DEV void big_dma_stage(uint8_t* slot, const uint8_t* const* a_src, const ui
 // A tiles mt (E4M3: 2 x 16 bytes, E2M1: 16 bytes; + scale each).
 template <int AFMT>
 struct BigFrag {
-  v4i b[kWT];
-  v4i lo[4];
-  v4i hi[AFMT == 0 ? 4 : 1];
-  int sb[kWT], sa[4];
+  v4i b[Cfg<AFMT>::WT];
+  v4i lo[Cfg<AFMT>::TT];
+  v4i hi[AFMT == 0 ? Cfg<AFMT>::TT : 1];
+  int sb[Cfg<AFMT>::WT], sa[Cfg<AFMT>::TT];
 };
 
 // Reads one stage's fragments from ring slot L. S: the scale super-stage buffer, q0:
@@ -161,13 +185,13 @@ DSV4_DEV void big_read(BigFrag<AFMT>& F, const uint8_t* L, const uint8_t* S, int
                        int r32, int g2, int a_lo, int a_hi, int b_lane) {
   using C = Big<AFMT>;
 #pragma unroll
-  for (int nt = 0; nt < kWT; ++nt) {
+  for (int nt = 0; nt < Cfg<AFMT>::WT; ++nt) {
     F.b[nt] = *(const v4i*)(L + (C::ACH + brow0[nt] / 32) * 1024 + b_lane);
-    F.sb[nt] = scale_byte<true>(S, brow0[nt] + r32, q0 + g2);
+    F.sb[nt] = scale_byte<AFMT, true>(S, brow0[nt] + r32, q0 + g2);
   }
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const int row0 = 128 * wm + 32 * mt;
+  for (int mt = 0; mt < Cfg<AFMT>::TT; ++mt) {
+    const int row0 = (Cfg<AFMT>::BM / Cfg<AFMT>::WM) * wm + 32 * mt;
     if (AFMT == 0) {
       const uint8_t* ch = L + (row0 / 16 + (r32 >> 4)) * 1024;
       F.lo[mt] = *(const v4i*)(ch + a_lo);
@@ -175,7 +199,7 @@ DSV4_DEV void big_read(BigFrag<AFMT>& F, const uint8_t* L, const uint8_t* S, int
     } else {
       F.lo[mt] = *(const v4i*)(L + (row0 / 32) * 1024 + a_lo);
     }
-    F.sa[mt] = scale_byte<false>(S, row0 + r32, q0 + g2);
+    F.sa[mt] = scale_byte<AFMT, false>(S, row0 + r32, q0 + g2);
   }
 }
 
@@ -185,28 +209,29 @@ DSV4_DEV void big_read(BigFrag<AFMT>& F, const uint8_t* L, const uint8_t* S, int
 // the reads are done long before the next barrier waits for them.
 template <int AFMT>
 DSV4_DEV void big_sched() {
-  constexpr int kReads = AFMT == 0 ? 16 : 12;  // ds_reads of big_read
+  using G = Cfg<AFMT>;
+  constexpr int kReads = 2 * G::WT + (AFMT == 0 ? 3 : 2) * G::TT;  // ds_reads of big_read
 #pragma unroll
-  for (int i = 0; i < 4 * kWT; ++i) {
+  for (int i = 0; i < G::TT * G::WT; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA
     if (i < Big<AFMT>::L) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
     if (2 * i < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);    // DS read
   }
 }
 
-// One stage of MFMAs: 4 x 4 tiles of 32 x 32 per wave. The weights are the MFMA's A
+// One stage of MFMAs: TT x WT tiles of 32 x 32 per wave. The weights are the MFMA's A
 // operand and the activations its B operand, so accumulator (tt, wt) holds weight
 // columns x tokens: register r of lane l = weight column 8(r/4) + 4(l/32) + r%4 of
 // weight tile wt, token l%32 of token tile tt (the E4M3 B layout is the A layout).
 template <int AFMT>
-DSV4_DEV void big_mfma(v16f (&acc)[4][kWT], const BigFrag<AFMT>& F) {
+DSV4_DEV void big_mfma(v16f (&acc)[Cfg<AFMT>::TT][Cfg<AFMT>::WT], const BigFrag<AFMT>& F) {
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
+  for (int tt = 0; tt < Cfg<AFMT>::TT; ++tt) {
     const v4i lo = F.lo[tt];
     const v4i hi = AFMT == 0 ? F.hi[tt] : v4i{0, 0, 0, 0};
     const v8i xf = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
-    for (int wt = 0; wt < kWT; ++wt) {
+    for (int wt = 0; wt < Cfg<AFMT>::WT; ++wt) {
       const v8i wf = v8i{F.b[wt].x, F.b[wt].y, F.b[wt].z, F.b[wt].w, 0, 0, 0, 0};
       acc[tt][wt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf, xf, acc[tt][wt], 4, AFMT == 0 ? 0 : 4, 0,
                                                                    F.sb[wt], 0, F.sa[tt]);
@@ -218,7 +243,7 @@ DSV4_DEV void big_mfma(v16f (&acc)[4][kWT], const BigFrag<AFMT>& F) {
 // Each lane holds, per token tile tt, 4-column runs of one token's row (columns
 // 8q + 4(l/32) + e of every 32-column weight tile): SwiGLU, the quantisation blocks'
 // maxima (in-lane, then across the lane pair l, l ^ 32, then - FP8 h only - across the
-// four waves of a token row through the LDS) and the packing all stay in registers.
+// WN waves of a token row through the LDS) and the packing all stay in registers.
 // bf16 / E4M3 / E2M1 conversions use the gfx950 converters, which agree bit for bit
 // with the library's software quantisers on every input they see here (RNE; E4M3 after
 // the clamp to +-448; E2M1 with the sign of the input, whose -0 the rule-0 path
@@ -271,10 +296,11 @@ DSV4_DEV uint32_t pk_fp4x2(float a, float b, float inv, int rule) {
 // Block -> tile mapping. Workgroups are dispatched to the 8 XCDs round-robin by
 // linear id, and each XCD has its own L2, so with the plain mapping (N tiles fastest)
 // every XCD would run 2 of the 16 N tiles of every M block and fetch every M block's
-// A rows into its own L2. With N tiles a multiple of 8, the 32 consecutive
-// workgroups an XCD runs at once (one per CU) get 4 M blocks x 8 N tiles instead:
-// A rows shared 8 ways and weight tiles 4 ways within one L2. The grid's y extent
-// is then padded to a multiple of 32 M blocks; the padding blocks exit at once.
+// A rows into its own L2. With N tiles a multiple of 8, each 32 consecutive
+// workgroups of an XCD get 4 M extents x 8 N tiles instead: A rows shared 8 ways
+// and weight tiles 4 ways within one L2. (An M extent is a hot-layout block, or
+// half of one where a block takes two workgroups.) The grid's y extent is then
+// padded to a multiple of 32; the padding workgroups exit at once.
 DSV4_DEV void big_tile_of_block(int& mb, int& nt) {
   const int ntiles = gridDim.x;
   if (ntiles % 8 != 0) {
@@ -291,21 +317,24 @@ DSV4_DEV void big_tile_of_block(int& mb, int& nt) {
 }
 
 template <int AFMT, bool GATEUP>
-__global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
+__global__ __launch_bounds__(Cfg<AFMT>::NT, Cfg<AFMT>::WGS) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
   using C = Big<AFMT>;
+  using G = Cfg<AFMT>;
+  constexpr int kBM = G::BM, H = G::WT / 2;  // H: gate (and up) tiles per wave of gate/up
   __shared__ __attribute__((aligned(16))) uint8_t lds[C::LDS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
-  int mb, nt;
-  big_tile_of_block(mb, nt);
-  if (mb * kBM >= p.num_post_padded[0]) return;  // also every block of the grid's padding
+  const int wm = wave / G::WN, wn = wave % G::WN;
+  int hb, nt;
+  big_tile_of_block(hb, nt);  // hb: this workgroup's share of a hot-layout block
+  const int mb = hb / G::WGS;
+  if (mb * kHB >= p.num_post_padded[0]) return;  // also every block of the grid's padding
   const int e = p.block_expert[mb];
   const Dsv4ExpertPtrs ex = p.experts[e];
   const bool have_w = GATEUP ? (ex.w1p && ex.w1s && ex.w3p && ex.w3s) : (ex.w2p && ex.w2s);
   const int NST = p.Kdim / kKS;
   const int wrow_bytes = p.Kdim / 2, srow = p.Kdim / 32;
   const int c0 = nt * (GATEUP ? 128 : 256);  // first intermediate column / output row of W2
-  const int slot0 = mb * kBM;
+  const int slot0 = mb * kHB + (hb % G::WGS) * kBM;
 
   // this lane's A piece per A load (stage 0): chunk wave * AV + v
   const uint8_t* a_src[C::AV];
@@ -333,13 +362,15 @@ __global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
                           : (int64_t)(16 * gtile + r) * wrow_bytes + 16 * ji);
   }
   // this lane's scale pieces (super-stage 0): piece q = (wave * SV + v) * 64 + lane of a
-  // buffer: A rows for q < 512, weight rows after; half (q / 256) % 2, row q % 256
+  // buffer: A rows for q < 2 kBM (half q / kBM, row q % kBM), weight rows after
   const uint8_t* sc_src[C::SV];
 #pragma unroll
   for (int v = 0; v < C::SV; ++v) {
     const int q = (wave * C::SV + v) * 64 + lane;
-    const int half = (q >> 8) & 1, row = q & 255;
-    if (q < 2 * kBM) {
+    const bool arow_piece = q < 2 * kBM;
+    const int w = arow_piece ? q : q - 2 * kBM, n = arow_piece ? kBM : kBN;
+    const int half = w / n, row = w % n;
+    if (arow_piece) {
       const int f = p.sorted_ids[slot0 + row];
       const int arow = f < p.R ? f / p.a_row_div : 0;
       sc_src[v] = p.a_scale + (int64_t)arow * srow + 16 * half;
@@ -349,26 +380,27 @@ __global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
     }
   }
 
-  v16f acc[4][kWT];
+  v16f acc[G::TT][G::WT];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < G::TT; ++mt)
 #pragma unroll
-    for (int nt = 0; nt < kWT; ++nt) acc[mt][nt] = v16f{};
+    for (int nt = 0; nt < G::WT; ++nt) acc[mt][nt] = v16f{};
   const int r32 = lane & 31, g2 = lane >> 5;
   // flat index (and gate/up: routing weight) of this lane's token in each token tile
-  int fr[4];
-  float wr[4];
+  int fr[G::TT];
+  float wr[G::TT];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    fr[tt] = p.sorted_ids[slot0 + 128 * wm + 32 * tt + r32];
+  for (int tt = 0; tt < G::TT; ++tt) {
+    fr[tt] = p.sorted_ids[slot0 + (kBM / G::WM) * wm + 32 * tt + r32];
     wr[tt] = GATEUP && fr[tt] < p.R ? p.topk_w[fr[tt]] : 0.0f;
   }
   // first weight row of this wave's 32-row tile nt in the block
-  // gate/up: tile 0 = gate rows 32 wn.., tile 1 = the matching up rows 128 + 32 wn..;
-  // down: output rows 64 wn + 32 nt..
-  int brow0[kWT];
+  // gate/up: tiles h < H = gate rows 32 (H wn + h).., tiles H + h = the matching up
+  // rows 128 + 32 (H wn + h)..; down: output rows 32 (WT wn + nt)..
+  int brow0[G::WT];
 #pragma unroll
-  for (int nt = 0; nt < kWT; ++nt) brow0[nt] = GATEUP ? nt * 128 + 32 * wn : 64 * wn + 32 * nt;
+  for (int nt = 0; nt < G::WT; ++nt)
+    brow0[nt] = GATEUP ? (nt / H) * 128 + 32 * (H * wn + nt % H) : 32 * (G::WT * wn + nt);
   // this lane's byte offsets inside a chunk (the swizzles of the layout comment)
   int a_lo, a_hi;
   if (AFMT == 0) {
@@ -434,86 +466,106 @@ __global__ __launch_bounds__(kNT, 1) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
 
   // epilogue (every wave is past the ring: the LDS is free)
   if (GATEUP) {
-    const int cw = c0 + 32 * wn;  // this wave's 32 intermediate columns
-    // h for columns cw + 8 q + 4 g2 + e of token tile tt, packed bf16 pairs
-    uint32_t hp[4][4][2];
-    float rmax[4];
+    const int cw = c0 + 32 * H * wn;  // this wave's first of 32 H intermediate columns
+    // h for columns cw + 32 h + 8 q + 4 g2 + e of token tile tt, packed bf16 pairs
+    uint32_t hp[G::TT][H][4][2];
+    float rmax[G::TT][H];  // per 32-column block, this lane's half of it
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt) {
-      float m = 0.0f;
+    for (int tt = 0; tt < G::TT; ++tt)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+      for (int h = 0; h < H; ++h) {
+        float m = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 4; e += 2) {
-          const int r = 4 * q + e;
-          // gate (tile 0) and up (tile 1) of the same column, rounded to bf16
-          const uint32_t gu0 = pk_bf16(acc[tt][0][r], acc[tt][1][r]);
-          const uint32_t gu1 = pk_bf16(acc[tt][0][r + 1], acc[tt][1][r + 1]);
-          const uint32_t hw = pk_bf16(big_swiglu(bf16_lo(gu0), bf16_hi(gu0), wr[tt], p.swiglu_limit),
-                                      big_swiglu(bf16_lo(gu1), bf16_hi(gu1), wr[tt], p.swiglu_limit));
-          hp[tt][q][e >> 1] = hw;
-          m = fmaxf(m, fmaxf(fabsf(bf16_lo(hw)), fabsf(bf16_hi(hw))));
-        }
-      rmax[tt] = m;
-    }
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; e += 2) {
+            const int r = 4 * q + e;
+            // gate (tile h) and up (tile H + h) of the same column, rounded to bf16
+            const uint32_t gu0 = pk_bf16(acc[tt][h][r], acc[tt][H + h][r]);
+            const uint32_t gu1 = pk_bf16(acc[tt][h][r + 1], acc[tt][H + h][r + 1]);
+            const uint32_t hw = pk_bf16(big_swiglu(bf16_lo(gu0), bf16_hi(gu0), wr[tt], p.swiglu_limit),
+                                        big_swiglu(bf16_lo(gu1), bf16_hi(gu1), wr[tt], p.swiglu_limit));
+            hp[tt][h][q][e >> 1] = hw;
+            m = fmaxf(m, fmaxf(fabsf(bf16_lo(hw)), fabsf(bf16_hi(hw))));
+          }
+        rmax[tt][h] = m;
+      }
     if (!p.hq_skip_h && p.out) {
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
+      for (int tt = 0; tt < G::TT; ++tt)
         if (fr[tt] < p.R)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            typedef uint32_t v2u __attribute__((ext_vector_type(2)));
-            *(v2u*)(p.out + (int64_t)fr[tt] * p.N + cw + 8 * q + 4 * g2) = v2u{hp[tt][q][0], hp[tt][q][1]};
-          }
+          for (int h = 0; h < H; ++h)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+              *(v2u*)(p.out + (int64_t)fr[tt] * p.N + cw + 32 * h + 8 * q + 4 * g2) =
+                  v2u{hp[tt][h][q][0], hp[tt][h][q][1]};
+            }
     }
-    if (p.hq_mode == 2) {  // MXFP4 h: one 32-column block per token tile, half of it in each lane of a pair
+    if (p.hq_mode == 2) {  // MXFP4 h: one 32-column block per (tt, h), half of it in each lane of a pair
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const int k = dsv4::mxfp4_block_exp(max_pair(rmax[tt]), p.hq_rule);
-        const float inv = dsv4::pow2f(-k);
-        if (fr[tt] < p.R) {
+      for (int tt = 0; tt < G::TT; ++tt)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t w0 = hp[tt][q][0], w1 = hp[tt][q][1];
-            const uint32_t nib = pk_fp4x2(bf16_lo(w0), bf16_hi(w0), inv, p.hq_rule) |
-                                 pk_fp4x2(bf16_lo(w1), bf16_hi(w1), inv, p.hq_rule) << 8;
-            *(uint16_t*)(p.hq_codes + (int64_t)fr[tt] * (p.N / 2) + (cw + 8 * q + 4 * g2) / 2) = (uint16_t)nib;
+        for (int h = 0; h < H; ++h) {
+          const int k = dsv4::mxfp4_block_exp(max_pair(rmax[tt][h]), p.hq_rule);
+          const float inv = dsv4::pow2f(-k);
+          if (fr[tt] < p.R) {
+            const int col = cw + 32 * h;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t w0 = hp[tt][h][q][0], w1 = hp[tt][h][q][1];
+              const uint32_t nib = pk_fp4x2(bf16_lo(w0), bf16_hi(w0), inv, p.hq_rule) |
+                                   pk_fp4x2(bf16_lo(w1), bf16_hi(w1), inv, p.hq_rule) << 8;
+              *(uint16_t*)(p.hq_codes + (int64_t)fr[tt] * (p.N / 2) + (col + 8 * q + 4 * g2) / 2) = (uint16_t)nib;
+            }
+            if (g2 == 0) p.hq_scale[(int64_t)fr[tt] * (p.N / 32) + col / 32] = (uint8_t)(k + 127);
           }
-          if (g2 == 0) p.hq_scale[(int64_t)fr[tt] * (p.N / 32) + cw / 32] = (uint8_t)(k + 127);
         }
-      }
-    } else if (p.hq_mode == 1) {  // FP8 h: one 128-column block per token, split over the four wn waves
-      float* am = (float*)lds;     // [4 wn][256 rows]
+    } else if (p.hq_mode == 1) {  // FP8 h: one 128-column block per token, split over the WN waves of a row
+      float* am = (float*)lds;     // [WN][kBM rows]
+      float bm[G::TT];
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        rmax[tt] = max_pair(rmax[tt]);
-        if (g2 == 0) am[wn * 256 + 128 * wm + 32 * tt + r32] = rmax[tt];
+      for (int tt = 0; tt < G::TT; ++tt) {
+        float m = rmax[tt][0];
+#pragma unroll
+        for (int h = 1; h < H; ++h) m = fmaxf(m, rmax[tt][h]);
+        if (g2 == 0) am[wn * kBM + (kBM / G::WM) * wm + 32 * tt + r32] = max_pair(m);
       }
       __syncthreads();
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const int row = 128 * wm + 32 * tt + r32;
-        const float bm = fmaxf(fmaxf(am[row], am[256 + row]), fmaxf(am[512 + row], am[768 + row]));
-        const int k = dsv4::fp8_block_exp(bm);
+      for (int tt = 0; tt < G::TT; ++tt) {
+        const int row = (kBM / G::WM) * wm + 32 * tt + r32;
+        bm[tt] = am[row];
+#pragma unroll
+        for (int w = 1; w < G::WN; ++w) bm[tt] = fmaxf(bm[tt], am[w * kBM + row]);
+      }
+#pragma unroll
+      for (int tt = 0; tt < G::TT; ++tt) {
+        const int k = dsv4::fp8_block_exp(bm[tt]);
         const float inv = dsv4::pow2f(-k);
         if (fr[tt] < p.R) {
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const uint32_t w0 = hp[tt][q][0], w1 = hp[tt][q][1];
-            *(uint32_t*)(p.hq_codes + (int64_t)fr[tt] * p.N + cw + 8 * q + 4 * g2) =
-                pk_fp8x4(bf16_lo(w0), bf16_hi(w0), bf16_lo(w1), bf16_hi(w1), inv);
-          }
-          if (g2 == 0) p.hq_scale[(int64_t)fr[tt] * (p.N / 32) + cw / 32] = (uint8_t)(k + 127);
+          for (int h = 0; h < H; ++h)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t w0 = hp[tt][h][q][0], w1 = hp[tt][h][q][1];
+              *(uint32_t*)(p.hq_codes + (int64_t)fr[tt] * p.N + cw + 32 * h + 8 * q + 4 * g2) =
+                  pk_fp8x4(bf16_lo(w0), bf16_hi(w0), bf16_lo(w1), bf16_hi(w1), inv);
+            }
+          if (g2 == 0)
+#pragma unroll
+            for (int h = 0; h < H; ++h) p.hq_scale[(int64_t)fr[tt] * (p.N / 32) + cw / 32 + h] = (uint8_t)(k + 127);
         }
       }
     }
   } else {
-    const int cw = c0 + 64 * wn;  // this wave's first output column
+    const int cw = c0 + 32 * G::WT * wn;  // this wave's first output column
 #pragma unroll
-    for (int tt = 0; tt < 4; ++tt)
+    for (int tt = 0; tt < G::TT; ++tt)
       if (fr[tt] < p.R)
 #pragma unroll
-        for (int wt = 0; wt < kWT; ++wt)
+        for (int wt = 0; wt < G::WT; ++wt)
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             typedef uint32_t v2u __attribute__((ext_vector_type(2)));
@@ -531,19 +583,22 @@ bool moe_gemm_big_supported(int kdim, int n, bool gateup) {
   return kdim >= 1024 && kdim % 1024 == 0 && n % (gateup ? 128 : 256) == 0;
 }
 
+template <int AFMT>
+static void launch_big(const Dsv4GemmArgs& a, bool gateup, int ntiles, hipStream_t st) {
+  using G = Cfg<AFMT>;
+  // workgroups' M extent: WGS per hot-layout block, in whole groups of 32 for the XCD
+  // grouping of big_tile_of_block
+  const int m = G::WGS * a.max_blocks;
+  const dim3 grid(ntiles, ntiles % 8 == 0 ? (m + 31) / 32 * 32 : m);
+  if (gateup) hipLaunchKernelGGL((moe_gemm_big_kernel<AFMT, true>), grid, dim3(G::NT), 0, st, a);
+  else hipLaunchKernelGGL((moe_gemm_big_kernel<AFMT, false>), grid, dim3(G::NT), 0, st, a);
+}
+
 hipError_t launch_moe_gemm_big(const Dsv4GemmArgs& a, bool gateup, hipStream_t st) {
-  if (a.block_m != kBM || !moe_gemm_big_supported(a.Kdim, a.N, gateup)) return hipErrorInvalidValue;
+  if (a.block_m != kHB || !moe_gemm_big_supported(a.Kdim, a.N, gateup)) return hipErrorInvalidValue;
   if (a.max_blocks <= 0) return hipSuccess;
   const int ntiles = a.N / (gateup ? 128 : 256);
-  // the XCD grouping of big_tile_of_block needs M blocks in whole groups of 32
-  const int mblocks = ntiles % 8 == 0 ? (a.max_blocks + 31) / 32 * 32 : a.max_blocks;
-  const dim3 grid(ntiles, mblocks);
-  if (gateup) {
-    if (a.afmt == 0) hipLaunchKernelGGL((moe_gemm_big_kernel<0, true>), grid, dim3(kNT), 0, st, a);
-    else hipLaunchKernelGGL((moe_gemm_big_kernel<1, true>), grid, dim3(kNT), 0, st, a);
-  } else {
-    if (a.afmt == 0) hipLaunchKernelGGL((moe_gemm_big_kernel<0, false>), grid, dim3(kNT), 0, st, a);
-    else hipLaunchKernelGGL((moe_gemm_big_kernel<1, false>), grid, dim3(kNT), 0, st, a);
-  }
+  if (a.afmt == 0) launch_big<0>(a, gateup, ntiles, st);
+  else launch_big<1>(a, gateup, ntiles, st);
   return hipGetLastError();
 }
