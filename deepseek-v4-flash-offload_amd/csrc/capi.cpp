@@ -382,28 +382,32 @@ struct LayerWs {
   int64_t sorted_ids_h, block_expert_h, npp_h;
 };
 
-// Experts with at least hot_rows_threshold(R) routed rows run in 256-row blocks on
+// Experts with at least hot_rows_threshold() routed rows run in 256-row blocks on
 // the large-tile kernel in layers of at least hot_layer_rows() routed rows; the rest
 // keep 64-row blocks. Measured with Zipf(1.1) routing over 256 experts (hidden 4096,
-// inter 2048) and the eight-wave large-tile kernel: the two-launch split lost 10 % at
-// 2048 tokens (the hot experts' blocks too few to fill a launch of their own) and
-// gained 2 % (bf16) / 5.5 % (a4w4) at 4096 tokens with a 256-row threshold; from 8192
-// tokens a 128-row threshold was 2-3 % faster than 256 (which the 4096-token layer
-// preferred). DSV4_HOT_LAYER_ROWS and DSV4_HOT_ROWS (0: never) override them, read once.
-static int64_t hot_layer_rows() {
+// inter 2048), top-8:
+//   a4w4 (one 8-wave workgroup per hot block): the split lost 5-10 % at 2048 tokens
+//   (the hot experts' blocks too few to fill a launch of their own) and gained 5.5 %
+//   at 4096 tokens with a 256-row threshold (2 % ahead of 128); from 8192 tokens a
+//   128-row threshold was 2-3 % faster than 256.
+//   bf16 (two half-block workgroups per hot block, twice the workgroups per launch):
+//   with a 128-row threshold the split gained 1.5-2 % at 2048 and 4096 tokens, where a
+//   256-row threshold lost 1 % and 0.5-1.5 % against it.
+// DSV4_HOT_LAYER_ROWS and DSV4_HOT_ROWS (0: never) override them, read once.
+static int64_t hot_layer_rows(bool fp8) {
   static const int64_t v = [] {
     const char* s = getenv("DSV4_HOT_LAYER_ROWS");
-    return s ? (int64_t)atoll(s) : (int64_t)32768;
+    return s ? (int64_t)atoll(s) : (int64_t)-1;
   }();
-  return v;
+  return v >= 0 ? v : (fp8 ? 16384 : 32768);
 }
 
-static int hot_rows_threshold(int64_t R) {
+static int hot_rows_threshold(int64_t R, bool fp8) {
   static const int v = [] {
     const char* s = getenv("DSV4_HOT_ROWS");
     return s ? atoi(s) : -1;
   }();
-  return v >= 0 ? v : (R >= 65536 ? 128 : 256);
+  return v >= 0 ? v : (fp8 || R >= 65536 ? 128 : 256);
 }
 
 // Rows per M block: 16 (decode kernel, ~1-4 rows per active expert) below 2048
@@ -438,8 +442,8 @@ static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool sha
   w.out = take(2 * Rt * D);
   w.align_scratch = R > kAlignSmallRows ? take(align_chunked_scratch_bytes((int)R, E)) : 0;
   w.route_part = routed ? take(dsv4_moe_route_workspace_bytes(T, D, E)) : -1;  // router partial logits
-  const int hot = hot_rows_threshold(R);
-  if (!pure && R >= hot_layer_rows() && R > kAlignSmallRows && hot > 0 && moe_gemm_big_supported(D, I, true) &&
+  const int hot = hot_rows_threshold(R, fp8);
+  if (!pure && R >= hot_layer_rows(fp8) && R > kAlignSmallRows && hot > 0 && moe_gemm_big_supported(D, I, true) &&
       moe_gemm_big_supported(I, D, false)) {
     w.hot_min = hot;
     // each hot expert holds >= hot_min rows: blocks <= R/256 + min(E, R/hot_min) + 1

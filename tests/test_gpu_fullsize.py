@@ -73,7 +73,7 @@ def test_full_size_layer_on_sampled_tokens(gpu, profile, T):
                        profile=prof, rule=RULE_OCP_FLOOR)
     torch.cuda.synchronize()
     got_all = Q.bf16_bits_to_f32(_bits(y))
-    sample = _sample_tokens(ids, T)
+    sample = _sample_tokens(ids, T, profile)
     print(f"full size {profile} T={T}: checking {sample.size} tokens", flush=True)
     host = {int(e): {k: v.cpu().numpy() for k, v in experts[int(e)].items()} for e in np.unique(ids[sample])}
     if profile == "bf16":
@@ -95,25 +95,30 @@ def test_full_size_layer_on_sampled_tokens(gpu, profile, T):
     del experts, tiled
 
 
-def _sample_tokens(ids, T, n_hot=16, n_random=32):
+def _sample_tokens(ids, T, profile, n_hot=16, n_random=32):
     """Tokens of the first and last routed row of every M block of the n_hot
     hottest experts (rows of an expert in flat-index order, blocks of the
-    layer's block size: 64 rows from 2048 routed rows on, else 16; 256 for the
-    experts the large-tile split takes - at least 256 rows from 32,768 routed
-    rows on, at least 128 from 65,536 - where only the 8 hottest are taken),
-    plus n_random random tokens; every token when T <= 64."""
+    layer's block size: 64 rows from 2048 routed rows on, else 16), plus
+    n_random random tokens; every token when T <= 64. The large-tile split
+    (only the 8 hottest experts are then taken) gives its experts blocks of
+    the rows one workgroup takes: a4w4 from 32,768 routed rows, experts with
+    at least 256 rows (128 from 65,536), 256 rows; bf16 from 16,384 routed
+    rows, experts with at least 128 rows, 128 rows (half a hot block)."""
     if T <= 64:
         return np.arange(T)
     R = ids.size
     flat = ids.reshape(-1)
     counts = np.bincount(flat, minlength=E)
     picks = set()
-    hot_min = 128 if R >= 65536 else 256  # the layer's large-tile split (256-row blocks)
-    if R >= 32768:
+    fp8 = profile == "bf16"
+    split = R >= (16384 if fp8 else 32768)  # the layer's large-tile split
+    hot_min = 128 if (fp8 or R >= 65536) else 256
+    if split:
         n_hot = 8
     for e in np.argsort(-counts, kind="stable")[:n_hot]:
         tok = np.nonzero(flat == e)[0] // ids.shape[1]
-        bm = 256 if (R >= 32768 and tok.size >= hot_min) else (64 if R >= 2048 else 16)
+        big = 128 if fp8 else 256
+        bm = big if (split and tok.size >= hot_min) else (64 if R >= 2048 else 16)
         for b in range(0, tok.size, bm):
             picks.add(int(tok[b]))
             picks.add(int(tok[min(b + bm, tok.size) - 1]))
