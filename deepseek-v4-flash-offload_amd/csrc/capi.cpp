@@ -481,10 +481,66 @@ constexpr int kFusedRouteTokens = 16;
 // The routed layer, and with `shared` the shared expert as one more group of
 // T rows (bf16 profile only; checked by the caller). With `route` the layer
 // first routes x itself: topk_ids / topk_w are then the route's outputs.
+// The hot layout's two large-tile launches run on a side stream, concurrently with the
+// main layout's launches: the tiled kernel streams the cold experts' weights (bound by
+// memory) while the large-tile kernel multiplies (bound by the MFMAs), and the two
+// write disjoint rows of h and of the down outputs. One side stream (default priority)
+// and a fork/join event pair per device, created on the device's first split layer;
+// a per-device mutex orders the callers that share them. DSV4_HOT_CONCURRENT=0 keeps
+// every launch on the caller's stream; read once.
+struct SideStream {
+  hipStream_t s;
+  hipEvent_t fork, join;
+  std::mutex mu;
+};
+static constexpr int kMaxSideDevices = 64;
+static std::mutex g_side_mu;
+static SideStream* g_side[kMaxSideDevices] = {};
+
+static bool hot_concurrent() {
+  static const bool v = [] {
+    const char* s = getenv("DSV4_HOT_CONCURRENT");
+    return !s || atoi(s) != 0;
+  }();
+  return v;
+}
+
+static int side_stream(void* stream, SideStream** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return hip_status(e, "layer: hipGetDevice");
+  hipDevice_t dev = cur;
+  if (stream) {
+    e = hipStreamGetDevice((hipStream_t)stream, &dev);
+    if (e != hipSuccess) return hip_status(e, "layer: hipStreamGetDevice");
+  }
+  REQUIRE(dev >= 0 && dev < kMaxSideDevices, DSV4_ERR_UNSUPPORTED, "layer: device %d beyond %d", (int)dev,
+          kMaxSideDevices);
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  if (!g_side[dev]) {
+    if (dev != cur) {
+      e = hipSetDevice(dev);
+      if (e != hipSuccess) return hip_status(e, "layer: hipSetDevice");
+    }
+    SideStream* ss = new SideStream();
+    e = hipStreamCreateWithFlags(&ss->s, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ss->fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&ss->join, hipEventDisableTiming);
+    if (dev != cur) (void)hipSetDevice(cur);
+    if (e != hipSuccess) {
+      delete ss;  // the handles made so far stay with the runtime until the process ends
+      return hip_status(e, "layer: side stream / events");
+    }
+    g_side[dev] = ss;
+  }
+  *out = g_side[dev];
+  return DSV4_OK;
+}
+
 static int layer_forward(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
                          const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
                          const Dsv4ExpertPtrs* shared, float swiglu_limit, void* workspace, int64_t workspace_bytes,
-                         void* y, void* stream, const LayerRoute* route = nullptr) {
+                         void* y, void* stream, const LayerRoute* route = nullptr, bool one_stream = false) {
   if (route) {
     topk_ids = route->out_ids;
     ids_int64 = 0;
@@ -598,8 +654,6 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
     gu.shared_a_rows = n_sh;
     gu.shared = *shared;
   }
-  rc = hip_status(launch_moe_gemm_gateup(gu, (hipStream_t)stream), "gemm gate/up launch");
-  if (rc) return rc;
   // the hot layout's 256-row blocks (routed rows only) on the large-tile kernel
   auto hot_args = [&](Dsv4GemmArgs g) {
     g.sorted_ids = hot.sorted_ids;
@@ -610,8 +664,28 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
     g.has_shared = 0;
     return g;
   };
-  if (w.hot_min > 0) {
-    rc = hip_status(launch_moe_gemm_gateup(hot_args(gu), (hipStream_t)stream), "gemm gate/up (large tiles) launch");
+  // concurrent split: h is quantised in the epilogues (no h-quantisation launch
+  // between the two GEMMs reads the hot rows), so the hot rows' gate/up and down
+  // need nothing from the main stream after the align
+  SideStream* side = nullptr;
+  std::unique_lock<std::mutex> side_lock;
+  if (w.hot_min > 0 && hq_fused && !one_stream && hot_concurrent()) {
+    rc = side_stream(stream, &side);
+    if (rc) return rc;
+    side_lock = std::unique_lock<std::mutex>(side->mu);
+    rc = hip_status(hipEventRecord(side->fork, (hipStream_t)stream), "layer: fork record");
+    if (!rc) rc = hip_status(hipStreamWaitEvent(side->s, side->fork, 0), "layer: fork wait");
+    if (rc) return rc;
+  }
+  const hipStream_t hot_stream = side ? side->s : (hipStream_t)stream;
+  if (side) {
+    rc = hip_status(launch_moe_gemm_gateup(hot_args(gu), hot_stream), "gemm gate/up (large tiles) launch");
+    if (rc) return rc;
+  }
+  rc = hip_status(launch_moe_gemm_gateup(gu, (hipStream_t)stream), "gemm gate/up launch");
+  if (rc) return rc;
+  if (w.hot_min > 0 && !side) {
+    rc = hip_status(launch_moe_gemm_gateup(hot_args(gu), hot_stream), "gemm gate/up (large tiles) launch");
     if (rc) return rc;
   }
   if (!hq_fused && !pure) {  // FP8 blocks of 128 columns span four single-wave workgroups
@@ -639,10 +713,15 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
     dn.shared_expert = E;
     dn.shared = *shared;
   }
+  if (w.hot_min > 0) {
+    rc = hip_status(launch_moe_gemm_down(hot_args(dn), hot_stream), "gemm down (large tiles) launch");
+    if (rc) return rc;
+  }
   rc = hip_status(launch_moe_gemm_down(dn, (hipStream_t)stream), "gemm down launch");
   if (rc) return rc;
-  if (w.hot_min > 0) {
-    rc = hip_status(launch_moe_gemm_down(hot_args(dn), (hipStream_t)stream), "gemm down (large tiles) launch");
+  if (side) {  // the combine reads the hot rows' down outputs
+    rc = hip_status(hipEventRecord(side->join, side->s), "layer: join record");
+    if (!rc) rc = hip_status(hipStreamWaitEvent((hipStream_t)stream, side->join, 0), "layer: join wait");
     if (rc) return rc;
   }
   // ids outside [0, E) were skipped by the align (never computed) and add nothing here
@@ -733,8 +812,9 @@ int dsv4_moe_layer_forward_noalloc(int profile, int scale_rule, const void* x, c
   void* ws = nullptr;
   int rc = scratch_address(stream, &ws);
   if (rc) return rc;
+  // one stream: this entry point creates nothing (no side stream or events)
   return layer_forward(profile, scale_rule, x, topk_ids, ids_int64, topk_w, T, K, E, D, I, expert_table, nullptr,
-                       swiglu_limit, ws, kScratchBytes, y, stream);
+                       swiglu_limit, ws, kScratchBytes, y, stream, nullptr, true);
 }
 
 int dsv4_expand_block_scales(const void* block_scales, int64_t n_rows, int64_t k, void* out, void* stream) {
