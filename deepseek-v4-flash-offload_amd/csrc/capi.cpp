@@ -393,13 +393,16 @@ struct LayerWs {
 //   bf16 (two half-block workgroups per hot block, twice the workgroups per launch):
 //   with a 128-row threshold the split gained 1.5-2 % at 2048 and 4096 tokens, where a
 //   256-row threshold lost 1 % and 0.5-1.5 % against it.
+//   a4w4 below 32,768 rows, where the large-tile launch takes half blocks as well and
+//   runs beside the tiled one: a 128-row threshold gained 3 % at 2048 tokens (1.011-1.018
+//   -> 0.981-0.984 ms), 256 lost 4 %.
 // DSV4_HOT_LAYER_ROWS and DSV4_HOT_ROWS (0: never) override them, read once.
-static int64_t hot_layer_rows(bool fp8) {
+static int64_t hot_layer_rows(bool /*fp8*/) {
   static const int64_t v = [] {
     const char* s = getenv("DSV4_HOT_LAYER_ROWS");
     return s ? (int64_t)atoll(s) : (int64_t)-1;
   }();
-  return v >= 0 ? v : (fp8 ? 16384 : 32768);
+  return v >= 0 ? v : 16384;
 }
 
 static int hot_rows_threshold(int64_t R, bool fp8) {
@@ -407,7 +410,7 @@ static int hot_rows_threshold(int64_t R, bool fp8) {
     const char* s = getenv("DSV4_HOT_ROWS");
     return s ? atoi(s) : -1;
   }();
-  return v >= 0 ? v : (fp8 || R >= 65536 ? 128 : 256);
+  return v >= 0 ? v : (fp8 || R < 32768 || R >= 65536 ? 128 : 256);
 }
 
 // Rows per M block: 16 (decode kernel, ~1-4 rows per active expert) below 2048

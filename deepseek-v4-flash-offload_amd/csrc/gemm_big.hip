@@ -62,16 +62,17 @@ constexpr int kBN = 256;     // weight rows per block
 constexpr int kKS = 64;      // k per stage
 constexpr int kSS = 16;      // stages per scale super-stage (1024 k)
 
-// Workgroup shape per activation format. E4M3 (bf16 profile): two workgroups per CU,
-// each half a 256-row block, 4 waves of 64 rows x 128 weight rows; E2M1 (a4w4): one
-// workgroup per CU over the whole block, 8 waves of 128 x 64. Either way two waves share
-// a SIMD; two independent workgroups let one's MFMAs run while the other waits at its
-// stage barrier. Measured at 16384 tokens (layer time, same runs): E4M3 4.49-4.60 ms with
-// the 8-wave shape against 4.27-4.29 with the half-block one; E2M1 3.66-3.68 with the
-// 8-wave shape against 3.73-3.76.
-template <int AFMT>
+// Workgroup shapes. HALF: two workgroups per CU, each half a 256-row block, 4 waves of
+// 64 rows x 128 weight rows; otherwise one workgroup per CU over the whole block, 8
+// waves of 128 x 64. Either way two waves share a SIMD; two independent workgroups let
+// one's MFMAs run while the other waits at its stage barrier. Measured (layer time, same
+// runs): E4M3 at 16384 tokens 4.49-4.60 ms with the 8-wave shape against 4.27-4.29 with
+// the half-block one; E2M1 at 16384 tokens 3.54-3.68 against 3.68-3.76, at 2048 tokens
+// (16,384 routed rows, the hot experts' blocks too few to fill the CUs) 1.012-1.022
+// against 0.981-0.984. launch_moe_gemm_big picks HALF for E4M3, and for E2M1 below
+// 32,768 rows.
+template <int AFMT, bool HALF>
 struct Cfg {
-  static constexpr bool HALF = AFMT == 0;
   static constexpr int BM = HALF ? 128 : 256;  // rows per workgroup
   static constexpr int NT = HALF ? 256 : 512;  // threads
   static constexpr int NW = NT / 64;           // waves
@@ -81,17 +82,19 @@ struct Cfg {
   static constexpr int WGS = HALF ? 2 : 1;     // workgroups per CU
 };
 
-template <int AFMT>
+template <int AFMT, bool HALF>
 struct Big {
-  static constexpr int kBM = Cfg<AFMT>::BM;
-  static constexpr int kNT = Cfg<AFMT>::NT;
+  using G = Cfg<AFMT, HALF>;
+  static constexpr int kBM = G::BM;
+  static constexpr int kNT = G::NT;
   static constexpr int ACH = kBM * (AFMT == 0 ? kKS : kKS / 2) / 1024;  // 1-KB A chunks per stage
   static constexpr int BCH = kBN * (kKS / 2) / 1024;  // 1-KB weight chunks per stage
   static constexpr int STAGE = (ACH + BCH) * 1024;
-  static constexpr int NB = AFMT == 0 ? 3 : 7;        // stage slots of the ring
-  static constexpr int AV = ACH / Cfg<AFMT>::NW;      // A loads per thread per stage
-  static constexpr int BV = BCH / Cfg<AFMT>::NW;      // weight loads per thread per stage
+  static constexpr int NB = HALF ? (AFMT == 0 ? 3 : 4) : (AFMT == 0 ? 5 : 7);  // stage slots of the ring
+  static constexpr int AV = ACH / Cfg<AFMT, HALF>::NW;      // A loads per thread per stage
+  static constexpr int BV = BCH / Cfg<AFMT, HALF>::NW;      // weight loads per thread per stage
   static constexpr int L = AV + BV;
+  typedef v16f Acc[G::TT][G::WT];  // a wave's accumulators
   // scales: one super-stage = 32 bytes per A row and per weight row (two 16-byte
   // pieces), loaded by LDS-DMA once per 16 stages into one of two buffers; a buffer
   // holds the A rows' then the weight rows' pieces, each half-major:
@@ -101,7 +104,7 @@ struct Big {
   static constexpr int BS_OFF = kBM * 32;            // weight rows within a buffer
   static constexpr int SV = SCL / (kNT * 16);         // scale loads per thread per super-stage
   static constexpr int LDS = NB * STAGE + 2 * SCL;
-  static_assert(LDS * Cfg<AFMT>::WGS <= 160 * 1024, "the stage ring and two scale super-stages must fit the LDS");
+  static_assert(LDS * Cfg<AFMT, HALF>::WGS <= 160 * 1024, "the stage ring and two scale super-stages must fit the LDS");
   static_assert(BCH == 8 && (ACH * 1024) == kBM * (AFMT == 0 ? kKS : kKS / 2), "chunking");
 };
 
@@ -136,28 +139,28 @@ DSV4_DEV void wait_loads_barrier() {
 
 // Issues the scale loads of super-stage ss into buffer `buf` (sc_src: this lane's
 // pieces at super-stage 0, in load order (wave * SV + v) * 64 + lane).
-template <int AFMT>
+template <int AFMT, bool HALF>
 DSV4_DEV void big_dma_scales(uint8_t* lds, int buf, const uint8_t* const* sc_src, int wave, int ss) {
-  using C = Big<AFMT>;
+  using C = Big<AFMT, HALF>;
 #pragma unroll
   for (int v = 0; v < C::SV; ++v) dma16(sc_src[v] + ss * 32, lds + C::AS_OFF + buf * C::SCL + (wave * C::SV + v) * 1024);
 }
 
 // The E8M0 byte q (0..31, the 32-k block within the super-stage) of row `row` of the
 // A (B = false) or weight (B = true) rows in scale buffer S.
-template <int AFMT, bool B>
+template <int AFMT, bool HALF, bool B>
 DSV4_DEV int scale_byte(const uint8_t* S, int row, int q) {
-  constexpr int kBM = Cfg<AFMT>::BM;
+  constexpr int kBM = Cfg<AFMT, HALF>::BM;
   return S[(B ? kBM * 32 : 0) + ((q >> 4) * (B ? kBN : kBM) + row) * 16 + (q & 15)];
 }
 
 // Issues stage s's loads into ring slot `slot`: this wave's A chunks wave * AV + v and
 // weight chunks wave * BV + v (a_src / b_src: this lane's piece at stage 0; bj / bg:
 // the weight offset per 4 stages / per stage within them, no branch in the loop).
-template <int AFMT>
+template <int AFMT, bool HALF>
 DSV4_DEV void big_dma_stage(uint8_t* slot, const uint8_t* const* a_src, const uint8_t* const* b_src, int wave,
                             int bj, int bg, int s) {
-  using C = Big<AFMT>;
+  using C = Big<AFMT, HALF>;
   const int aoff = s * (AFMT == 0 ? kKS : kKS / 2);
 #pragma unroll
   for (int v = 0; v < C::AV; ++v) dma16(a_src[v] + aoff, slot + (wave * C::AV + v) * 1024);
@@ -169,29 +172,29 @@ DSV4_DEV void big_dma_stage(uint8_t* slot, const uint8_t* const* a_src, const ui
 
 // The fragments of one stage for this wave: weight tiles nt (16 bytes + scale each),
 // A tiles mt (E4M3: 2 x 16 bytes, E2M1: 16 bytes; + scale each).
-template <int AFMT>
+template <int AFMT, bool HALF>
 struct BigFrag {
-  v4i b[Cfg<AFMT>::WT];
-  v4i lo[Cfg<AFMT>::TT];
-  v4i hi[AFMT == 0 ? Cfg<AFMT>::TT : 1];
-  int sb[Cfg<AFMT>::WT], sa[Cfg<AFMT>::TT];
+  v4i b[Cfg<AFMT, HALF>::WT];
+  v4i lo[Cfg<AFMT, HALF>::TT];
+  v4i hi[AFMT == 0 ? Cfg<AFMT, HALF>::TT : 1];
+  int sb[Cfg<AFMT, HALF>::WT], sa[Cfg<AFMT, HALF>::TT];
 };
 
 // Reads one stage's fragments from ring slot L. S: the scale super-stage buffer, q0:
 // this stage's first scale byte in it. a_lo / a_hi: this lane's byte offsets inside an
 // A chunk, b_lane inside a weight chunk.
-template <int AFMT>
-DSV4_DEV void big_read(BigFrag<AFMT>& F, const uint8_t* L, const uint8_t* S, int q0, int wm, const int* brow0,
+template <int AFMT, bool HALF>
+DSV4_DEV void big_read(BigFrag<AFMT, HALF>& F, const uint8_t* L, const uint8_t* S, int q0, int wm, const int* brow0,
                        int r32, int g2, int a_lo, int a_hi, int b_lane) {
-  using C = Big<AFMT>;
+  using C = Big<AFMT, HALF>;
 #pragma unroll
-  for (int nt = 0; nt < Cfg<AFMT>::WT; ++nt) {
+  for (int nt = 0; nt < Cfg<AFMT, HALF>::WT; ++nt) {
     F.b[nt] = *(const v4i*)(L + (C::ACH + brow0[nt] / 32) * 1024 + b_lane);
-    F.sb[nt] = scale_byte<AFMT, true>(S, brow0[nt] + r32, q0 + g2);
+    F.sb[nt] = scale_byte<AFMT, HALF, true>(S, brow0[nt] + r32, q0 + g2);
   }
 #pragma unroll
-  for (int mt = 0; mt < Cfg<AFMT>::TT; ++mt) {
-    const int row0 = (Cfg<AFMT>::BM / Cfg<AFMT>::WM) * wm + 32 * mt;
+  for (int mt = 0; mt < Cfg<AFMT, HALF>::TT; ++mt) {
+    const int row0 = (Cfg<AFMT, HALF>::BM / Cfg<AFMT, HALF>::WM) * wm + 32 * mt;
     if (AFMT == 0) {
       const uint8_t* ch = L + (row0 / 16 + (r32 >> 4)) * 1024;
       F.lo[mt] = *(const v4i*)(ch + a_lo);
@@ -199,7 +202,7 @@ DSV4_DEV void big_read(BigFrag<AFMT>& F, const uint8_t* L, const uint8_t* S, int
     } else {
       F.lo[mt] = *(const v4i*)(L + (row0 / 32) * 1024 + a_lo);
     }
-    F.sa[mt] = scale_byte<AFMT, false>(S, row0 + r32, q0 + g2);
+    F.sa[mt] = scale_byte<AFMT, HALF, false>(S, row0 + r32, q0 + g2);
   }
 }
 
@@ -207,14 +210,14 @@ DSV4_DEV void big_read(BigFrag<AFMT>& F, const uint8_t* L, const uint8_t* S, int
 // matrix pipe with FP8 A) followed by one of the stage's loads and two of the next
 // stage's fragment reads, so the LDS and the memory pipe work under the MFMAs and
 // the reads are done long before the next barrier waits for them.
-template <int AFMT>
+template <int AFMT, bool HALF>
 DSV4_DEV void big_sched() {
-  using G = Cfg<AFMT>;
+  using G = Cfg<AFMT, HALF>;
   constexpr int kReads = 2 * G::WT + (AFMT == 0 ? 3 : 2) * G::TT;  // ds_reads of big_read
 #pragma unroll
   for (int i = 0; i < G::TT * G::WT; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA
-    if (i < Big<AFMT>::L) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
+    if (i < Big<AFMT, HALF>::L) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // VMEM read
     if (2 * i < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);    // DS read
   }
 }
@@ -223,15 +226,15 @@ DSV4_DEV void big_sched() {
 // operand and the activations its B operand, so accumulator (tt, wt) holds weight
 // columns x tokens: register r of lane l = weight column 8(r/4) + 4(l/32) + r%4 of
 // weight tile wt, token l%32 of token tile tt (the E4M3 B layout is the A layout).
-template <int AFMT>
-DSV4_DEV void big_mfma(v16f (&acc)[Cfg<AFMT>::TT][Cfg<AFMT>::WT], const BigFrag<AFMT>& F) {
+template <int AFMT, bool HALF>
+DSV4_DEV void big_mfma(typename Big<AFMT, HALF>::Acc& acc, const BigFrag<AFMT, HALF>& F) {
 #pragma unroll
-  for (int tt = 0; tt < Cfg<AFMT>::TT; ++tt) {
+  for (int tt = 0; tt < Cfg<AFMT, HALF>::TT; ++tt) {
     const v4i lo = F.lo[tt];
     const v4i hi = AFMT == 0 ? F.hi[tt] : v4i{0, 0, 0, 0};
     const v8i xf = v8i{lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
 #pragma unroll
-    for (int wt = 0; wt < Cfg<AFMT>::WT; ++wt) {
+    for (int wt = 0; wt < Cfg<AFMT, HALF>::WT; ++wt) {
       const v8i wf = v8i{F.b[wt].x, F.b[wt].y, F.b[wt].z, F.b[wt].w, 0, 0, 0, 0};
       acc[tt][wt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf, xf, acc[tt][wt], 4, AFMT == 0 ? 0 : 4, 0,
                                                                    F.sb[wt], 0, F.sa[tt]);
@@ -316,10 +319,10 @@ DSV4_DEV void big_tile_of_block(int& mb, int& nt) {
   nt = 8 * (gi % ngroups) + (w & 7);
 }
 
-template <int AFMT, bool GATEUP>
-__global__ __launch_bounds__(Cfg<AFMT>::NT, Cfg<AFMT>::WGS) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
-  using C = Big<AFMT>;
-  using G = Cfg<AFMT>;
+template <int AFMT, bool HALF, bool GATEUP>
+__global__ __launch_bounds__((Cfg<AFMT, HALF>::NT), (Cfg<AFMT, HALF>::WGS)) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
+  using C = Big<AFMT, HALF>;
+  using G = Cfg<AFMT, HALF>;
   constexpr int kBM = G::BM, H = G::WT / 2;  // H: gate (and up) tiles per wave of gate/up
   __shared__ __attribute__((aligned(16))) uint8_t lds[C::LDS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -430,29 +433,29 @@ __global__ __launch_bounds__(Cfg<AFMT>::NT, Cfg<AFMT>::WGS) void moe_gemm_big_ke
     // flight before storing them (it cannot see that 16 stages have passed). NST =
     // K / 64 is a multiple of 16.
     const int NSS = NST / kSS;
-    big_dma_scales<AFMT>(lds, 0, sc_src, wave, 0);
+    big_dma_scales<AFMT, HALF>(lds, 0, sc_src, wave, 0);
 #pragma unroll
-    for (int t = 0; t < C::NB; ++t) big_dma_stage<AFMT>(lds + t * C::STAGE, a_src, b_src, wave, bj, bg, t);
+    for (int t = 0; t < C::NB; ++t) big_dma_stage<AFMT, HALF>(lds + t * C::STAGE, a_src, b_src, wave, bj, bg, t);
     wait_loads_barrier<C::L * (C::NB - 1)>();
-    BigFrag<AFMT> f0, f1;
-    big_read<AFMT>(f0, lds, lds + C::AS_OFF, 0, wm, brow0, r32, g2, a_lo, a_hi, b_lane);
+    BigFrag<AFMT, HALF> f0, f1;
+    big_read<AFMT, HALF>(f0, lds, lds + C::AS_OFF, 0, wm, brow0, r32, g2, a_lo, a_hi, b_lane);
     int slot = 0;  // ring slot of stage s
     // stage s: multiply Fc (stage s), read stage s + 1 into Fn
 #define DSV4_BIG_STEP(Fc, Fn)                                                                                  \
   {                                                                                                            \
     const int nslot = slot + 1 == C::NB ? 0 : slot + 1;                                                        \
     wait_loads_barrier<C::L * (C::NB - 2)>();                                                                  \
-    big_dma_stage<AFMT>(lds + slot * C::STAGE, a_src, b_src, wave, bj, bg, min(s + C::NB, NST - 1));            \
+    big_dma_stage<AFMT, HALF>(lds + slot * C::STAGE, a_src, b_src, wave, bj, bg, min(s + C::NB, NST - 1));            \
     const int s1 = s + 1;                                                                                      \
-    big_read<AFMT>(Fn, lds + nslot * C::STAGE, lds + C::AS_OFF + ((s1 / kSS) & 1) * C::SCL, 2 * (s1 % kSS),   \
+    big_read<AFMT, HALF>(Fn, lds + nslot * C::STAGE, lds + C::AS_OFF + ((s1 / kSS) & 1) * C::SCL, 2 * (s1 % kSS),   \
                    wm, brow0, r32, g2, a_lo, a_hi, b_lane);                                                    \
-    big_mfma<AFMT>(acc, Fc);                                                                                   \
-    big_sched<AFMT>();                                                                                         \
+    big_mfma<AFMT, HALF>(acc, Fc);                                                                                   \
+    big_sched<AFMT, HALF>();                                                                                         \
     slot = nslot;                                                                                              \
   }
 #pragma unroll 1
     for (int ss = 0; ss < NSS; ++ss) {
-      big_dma_scales<AFMT>(lds, (ss + 1) & 1, sc_src, wave, min(ss + 1, NSS - 1));
+      big_dma_scales<AFMT, HALF>(lds, (ss + 1) & 1, sc_src, wave, min(ss + 1, NSS - 1));
 #pragma unroll 1
       for (int s = kSS * ss; s < kSS * (ss + 1); ++s) {
         DSV4_BIG_STEP(f0, f1);
@@ -583,22 +586,25 @@ bool moe_gemm_big_supported(int kdim, int n, bool gateup) {
   return kdim >= 1024 && kdim % 1024 == 0 && n % (gateup ? 128 : 256) == 0;
 }
 
-template <int AFMT>
+template <int AFMT, bool HALF>
 static void launch_big(const Dsv4GemmArgs& a, bool gateup, int ntiles, hipStream_t st) {
-  using G = Cfg<AFMT>;
+  using G = Cfg<AFMT, HALF>;
   // workgroups' M extent: WGS per hot-layout block, in whole groups of 32 for the XCD
   // grouping of big_tile_of_block
   const int m = G::WGS * a.max_blocks;
   const dim3 grid(ntiles, ntiles % 8 == 0 ? (m + 31) / 32 * 32 : m);
-  if (gateup) hipLaunchKernelGGL((moe_gemm_big_kernel<AFMT, true>), grid, dim3(G::NT), 0, st, a);
-  else hipLaunchKernelGGL((moe_gemm_big_kernel<AFMT, false>), grid, dim3(G::NT), 0, st, a);
+  if (gateup) hipLaunchKernelGGL((moe_gemm_big_kernel<AFMT, HALF, true>), grid, dim3(G::NT), 0, st, a);
+  else hipLaunchKernelGGL((moe_gemm_big_kernel<AFMT, HALF, false>), grid, dim3(G::NT), 0, st, a);
 }
 
 hipError_t launch_moe_gemm_big(const Dsv4GemmArgs& a, bool gateup, hipStream_t st) {
   if (a.block_m != kHB || !moe_gemm_big_supported(a.Kdim, a.N, gateup)) return hipErrorInvalidValue;
   if (a.max_blocks <= 0) return hipSuccess;
   const int ntiles = a.N / (gateup ? 128 : 256);
-  if (a.afmt == 0) launch_big<0>(a, gateup, ntiles, st);
-  else launch_big<1>(a, gateup, ntiles, st);
+  // workgroup shape (Cfg): half blocks for E4M3, and for E2M1 while the layer's rows
+  // are too few to fill the CUs with whole blocks
+  if (a.afmt == 0) launch_big<0, true>(a, gateup, ntiles, st);
+  else if (a.R < 32768) launch_big<1, true>(a, gateup, ntiles, st);
+  else launch_big<1, false>(a, gateup, ntiles, st);
   return hipGetLastError();
 }

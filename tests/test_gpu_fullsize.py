@@ -100,10 +100,11 @@ def _sample_tokens(ids, T, profile, n_hot=16, n_random=32):
     hottest experts (rows of an expert in flat-index order, blocks of the
     layer's block size: 64 rows from 2048 routed rows on, else 16), plus
     n_random random tokens; every token when T <= 64. The large-tile split
-    (only the 8 hottest experts are then taken) gives its experts blocks of
-    the rows one workgroup takes: a4w4 from 32,768 routed rows, experts with
-    at least 256 rows (128 from 65,536), 256 rows; bf16 from 16,384 routed
-    rows, experts with at least 128 rows, 128 rows (half a hot block)."""
+    (from 16,384 routed rows; only the 8 hottest experts are then taken)
+    gives its experts blocks of the rows one workgroup takes: bf16, experts
+    with at least 128 rows, 128 rows (half a hot block); a4w4, experts with
+    at least 128 rows in 128-row halves below 32,768 routed rows, then at
+    least 256 rows (128 from 65,536) in whole 256-row blocks."""
     if T <= 64:
         return np.arange(T)
     R = ids.size
@@ -111,13 +112,13 @@ def _sample_tokens(ids, T, profile, n_hot=16, n_random=32):
     counts = np.bincount(flat, minlength=E)
     picks = set()
     fp8 = profile == "bf16"
-    split = R >= (16384 if fp8 else 32768)  # the layer's large-tile split
-    hot_min = 128 if (fp8 or R >= 65536) else 256
+    split = R >= 16384 and profile != "bf16_pure"  # the layer's large-tile split
+    hot_min = 128 if (fp8 or R < 32768 or R >= 65536) else 256
     if split:
         n_hot = 8
     for e in np.argsort(-counts, kind="stable")[:n_hot]:
         tok = np.nonzero(flat == e)[0] // ids.shape[1]
-        big = 128 if fp8 else 256
+        big = 128 if (fp8 or R < 32768) else 256
         bm = big if (split and tok.size >= hot_min) else (64 if R >= 2048 else 16)
         for b in range(0, tok.size, bm):
             picks.add(int(tok[b]))
