@@ -8,11 +8,14 @@
 // expert's slot - so every weight byte a workgroup brings from L2 serves 128 or
 // 256 rows (the 16/64-row kernels re-read an expert's weights once per 16 or 64
 // rows) and every A byte 256 weight rows. Two waves share each SIMD, each with
-// 128 accumulator registers of v_mfma_scale_f32_32x32x64_f8f6f4 tiles:
-//   E2M1 A (a4w4)  : one workgroup of 8 waves per CU over the whole 256-row block;
-//                    a wave owns 128 rows x 64 weight rows (4 x 2 tiles).
-//   E4M3 A (bf16)  : two workgroups of 4 waves per CU, each over half a block
-//                    (128 rows); a wave owns 64 rows x 128 weight rows (2 x 4).
+// 128 accumulator registers of v_mfma_scale_f32_32x32x64_f8f6f4 tiles, in one of
+// two shapes picked per launch (Cfg):
+//   whole blocks (E2M1 A from 32,768 rows): one workgroup of 8 waves per CU over
+//                    the whole 256-row block; a wave owns 128 rows x 64 weight rows
+//                    (4 x 2 tiles).
+//   half blocks (E4M3 A; E2M1 A below 32,768 rows): two workgroups of 4 waves per
+//                    CU, each over half a block (128 rows); a wave owns 64 rows x
+//                    128 weight rows (2 x 4).
 // A weight fragment read from LDS feeds TT MFMAs and an activation fragment WT.
 // Two waves per SIMD let one wave's MFMAs run while the other waits at a barrier
 // or on its LDS reads (against one 128 x 128 wave per SIMD, 256 accumulators in
@@ -24,7 +27,7 @@
 // Operands move global -> LDS with global_load_lds_dwordx4 (lane i of one
 // instruction writes its 16 bytes at the instruction's LDS base + 16 i): no
 // staging registers, so a ring of NB stage slots keeps NB - 1 stages of loads
-// in flight (96 KB per CU with E2M1 A and one workgroup, 2 x 48 KB with E4M3 A);
+// in flight (96 KB per CU with E2M1 A on whole blocks, 2 x 32-36 KB on half blocks);
 // the depth of the ring, and the second workgroup, hide the load latency.
 // Each 1-KB chunk is laid out in the order the MFMA lanes read it, with an XOR
 // swizzle that puts the 16 lanes of each ds_read_b128 pass on distinct banks.
