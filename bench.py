@@ -11,7 +11,8 @@ cycled through so consecutive steps do not re-read the same weights from the
 Prints ONE JSON line. ``value`` = decode tokens/s through the layer.
 ``roofline`` = the dominant kernel (gate/up GEMM) - algorithmic bytes per
 launch over its HIP-event-timed average duration, against 8 TB/s HBM.
-``cpu_baseline`` = the numpy oracle of the same layer on one host core.
+``cpu_baseline`` = the same layer on the host cores (min(cores, 16) threads): the
+torch CPU restatement of the reference path, with the numpy oracle beside it.
 ``extra`` = dequant GB/s (config-0 matrices), a4w4 decode (64 tokens),
 prefill (2048 tokens) in both profiles, and expert offload (8 layers x 256
 experts in pinned host memory, 512 device slots, 512 drifting-Zipf decode
@@ -62,6 +63,11 @@ def parse():
 
 
 WEIGHT_LAYOUT = "tiled"
+
+
+def progress(msg):
+    """One line on stderr per finished leg (the JSON result stays the only stdout line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
 def gen_layer_weights(dev, n_layers, gen):
@@ -210,7 +216,51 @@ def measure_dequant(dev, gen, n_mats=64, reps=5):
     e1.synchronize()
     tg = e0.elapsed_time(e1) * 1e-3 / reps
     gemv_bytes = n_mats * N * (K // 2 + K // 32) + 2 * K + 2 * n_mats * N
+    # ExpertBank.get's miss path (offload.py:77-84): one expert's w1 [I, D], w2 [D, I] and w3
+    # [I, D], MFMA-tiled as the slot records hold them, dequantised by ONE launch per expert
+    # (dsv4_mxfp4_dequant_bf16_multi). 16 distinct experts (1 GB) back to back; the launches
+    # are queued behind one batched dequant so that host time between calls is not timed.
+    import ctypes
+    from dsv4_hip import _lib
+    n_ex = 16
+    shapes = ((I, D), (D, I), (I, D))
+    fn = _lib.lib().dsv4_mxfp4_dequant_bf16_multi
+    P3, L3 = ctypes.c_void_p * 3, ctypes.c_int64 * 3
+    keep, calls = [], []
+    for _ in range(n_ex):
+        ts = [(torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=dev, generator=gen),
+               torch.randint(117, 128, (n, k // 32), dtype=torch.uint8, device=dev, generator=gen),
+               torch.empty((n, k), dtype=torch.bfloat16, device=dev)) for n, k in shapes]
+        keep.append(ts)
+        calls.append((3, P3(*[t[0].data_ptr() | _lib.TILED_WEIGHTS for t in ts]), P3(*[t[1].data_ptr() for t in ts]),
+                      P3(*[t[2].data_ptr() for t in ts]), L3(*[n for n, _ in shapes]), L3(*[k for _, k in shapes])))
+    st = _lib.stream_handle(dev)
+    for c in calls:
+        assert fn(*c, st) == 0
+    torch.cuda.synchronize()
+    tm = []
+    for _ in range(reps):
+        ops.dequant_mxfp4(big_p, big_s, out=big_o)          # keeps the GPU busy while the calls queue
+        e0.record()
+        for c in calls:
+            fn(*c, st)
+        e1.record()
+        e1.synchronize()
+        tm.append(e0.elapsed_time(e1) * 1e-3 / n_ex)
+    t_ex = float(np.median(tm))
+    ex_bytes = sum(n * k for n, k in shapes) * 2.53125
+    t0h = time.perf_counter()
+    for _ in range(reps):
+        for c in calls:
+            fn(*c, st)
+    torch.cuda.synchronize()
+    host_us = (time.perf_counter() - t0h) / (reps * n_ex) * 1e6
+    del keep
     return {"gbs": gbs_b, "frac_hbm": gbs_b / HBM_PEAK_GBS, "batched_us": tb * 1e6,
+            "expert_get_one_launch": {"us_per_expert": t_ex * 1e6, "gbs": ex_bytes / t_ex / 1e9,
+                                      "frac_hbm": ex_bytes / t_ex / 1e9 / HBM_PEAK_GBS,
+                                      "bytes_per_expert": ex_bytes, "experts": n_ex,
+                                      "us_per_call_host_inclusive": host_us},
             "per_matrix_call_gbs": per / t / 1e9, "us_per_matrix_call": t * 1e6,
             "bytes_per_matrix": per, "matrices": n_mats,
             "gemv_batched_us": tg * 1e6, "gemv_gbs": gemv_bytes / tg / 1e9,
@@ -472,28 +522,37 @@ def measure_router(dev, iters=200):
 
 
 def cpu_baseline(sample_steps=2, threads=None, min_seconds=10.0):
-    """numpy oracle of the same bf16 decode layer (8 tokens, top-8 of 256, hidden 4096,
-    inter 2048) on the host cores: experts spread over min(host cores, 16) threads,
-    single-threaded BLAS inside each."""
+    """The same bf16 decode layer (8 tokens, top-8 of 256, hidden 4096, inter 2048, every
+    active expert dequantised from MXFP4 per step, as the GPU reads packed weights) on the
+    host cores, two ways:
+    * ``value``: the torch CPU restatement of the reference path (oracle/torch_cpu.py:
+      per-group fp32 ``torch.matmul``), ``torch.set_num_threads(min(host cores, 16))``;
+    * ``numpy_oracle``: the numpy oracle, experts spread over that many threads with
+      single-threaded BLAS inside each."""
     from threadpoolctl import threadpool_limits
     from oracle import moe as M
+    from oracle import torch_cpu as TC
     from dsv4_hip import synth
     threads = threads or min(os.cpu_count() or 1, 16)
+    x, ids, w = synth.layer_inputs(8, 8, E, D)
+    xb = x.view(torch.int16).numpy().view(np.uint16)
+    experts = {int(e): synth.expert_weights(int(e), D, I) for e in np.unique(ids)}
+    saved = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        dt_t, n_t = _timed(lambda: TC.routed_bf16(xb, ids, w, experts), min_seconds, min_runs=sample_steps)
+    finally:
+        torch.set_num_threads(saved)
     with threadpool_limits(limits=1):
-        x, ids, w = synth.layer_inputs(8, 8, E, D)
-        xb = x.view(torch.int16).numpy().view(np.uint16)
-        experts = {int(e): synth.expert_weights(int(e), D, I) for e in np.unique(ids)}
-        M.routed_bf16(xb, ids, w, experts, n_experts=E, workers=threads)  # warm-up
-        t0 = time.perf_counter()
-        n = 0
-        while n < sample_steps or time.perf_counter() - t0 < min_seconds:
-            M.routed_bf16(xb, ids, w, experts, n_experts=E, workers=threads)
-            n += 1
-        dt = (time.perf_counter() - t0) / n
-    return {"value": 8.0 / dt, "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n} decode steps of the numpy oracle after one warm-up (8 tokens, "
-                      f"top-8, {len(experts)} active experts, bf16 profile), experts on {threads} threads; "
-                      f"{dt:.2f} s/step"}
+        dt, n = _timed(lambda: M.routed_bf16(xb, ids, w, experts, n_experts=E, workers=threads), min_seconds,
+                       min_runs=sample_steps)
+    return {"value": 8.0 / dt_t, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n_t} decode steps of the torch CPU restatement after one warm-up (8 tokens, top-8, "
+                      f"{len(experts)} active experts, bf16 profile, experts dequantised per step, per-group "
+                      f"fp32 torch.matmul), torch on {threads} threads; {dt_t:.2f} s/step",
+            "numpy_oracle": {"value": 8.0 / dt, "unit": "tokens/s", "cores": threads,
+                             "sample": f"{n} decode steps of the numpy float64 oracle after one warm-up, experts "
+                                       f"on {threads} threads; {dt:.2f} s/step"}}
 
 
 def _timed(fn, min_seconds, min_runs=1, warmup=True):
@@ -537,6 +596,7 @@ def cpu_baselines(threads=None, seconds=8.0):
     from oracle import moe as M
     from oracle import mxfp4 as Q
     from oracle.lru import LRUOracle
+    from oracle import torch_cpu as TC
     from dsv4_hip import synth
     threads = threads or min(os.cpu_count() or 1, 16)
     cpu_model = platform.processor() or platform.machine()
@@ -574,6 +634,19 @@ def cpu_baselines(threads=None, seconds=8.0):
             t3, n3 = _timed(fn, 0.0, warmup=False)
             out[name] = {"tokens_per_s": 2048 / t3, "ms_per_layer": t3 * 1e3, "tflops": flops3 / t3 / 1e12,
                          "sample": f"{n3} layer call(s), {len(ex3)} active experts"}
+        saved = torch.get_num_threads()
+        torch.set_num_threads(threads)
+        try:
+            with threadpool_limits(limits=threads):  # the torch restatement runs on every thread
+                for name, fn in (("config3_bf16_2048_torch", lambda: TC.routed_bf16(xb3, ids3, w3, ex3)),
+                                 ("config3_a4w4_2048_torch", lambda: TC.routed_a4w4(xb3, ids3, w3, ex3))):
+                    t3, n3 = _timed(fn, 0.0, warmup=False)
+                    out[name] = {"tokens_per_s": 2048 / t3, "ms_per_layer": t3 * 1e3,
+                                 "tflops": flops3 / t3 / 1e12,
+                                 "sample": f"{n3} layer call(s) of the torch CPU restatement, torch on "
+                                           f"{threads} threads"}
+        finally:
+            torch.set_num_threads(saved)
         del ex3
         # config 4: the offload workload's routing (8 layers, drifting Zipf, 512 slots) through
         # an LRU of packed experts; on the host every layer dequantises its active experts
@@ -650,7 +723,8 @@ def main():
             "metric": "MoE decode tok/s (bf16 profile, 256 experts top-8, hidden 4096, inter 2048)",
             "value": T / s, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "ms_per_step": s * 1e3, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-            "dtype": "fp8e4m3 x mxfp4 (fp32 accumulate)", "data": "synthetic",
+            "dtype": "fp8e4m3 x mxfp4 (scaled MFMA: exact products, fp32 sums that drop products >10-13 binades "
+                     "below their group's largest)", "data": "synthetic",
             "config": {"workload": "bf16-profile MoE decode layer: 8 tokens, 256 experts, top-8 Zipf(1.1), "
                                    "hidden 4096, inter 2048, MXFP4 experts resident in HBM",
                        "tokens": T, "topk": K, "experts": E, "hidden": D, "inter": I,
@@ -666,6 +740,7 @@ def main():
         }
         del pools, tables
         torch.cuda.empty_cache()
+        progress(f"decode: {s * 1e6:.1f} us per layer")
     else:
         line = {"metric": "profile helper", "value": None}
     extra = {}
@@ -673,6 +748,7 @@ def main():
         extra["bf16_pure_decode_8"] = pure_decode
     if not args.no_extra and args.only in ("", "dequant"):
         extra["dequant_config0"] = measure_dequant(dev, gen)
+        progress("dequant done")
         torch.cuda.empty_cache()
     if not args.no_extra and args.only in ("", "prefill", "prefill2048", "compute"):
         pools, tables = gen_layer_weights(dev, 2, gen)
@@ -700,26 +776,34 @@ def main():
                            "frac_mfma_peak": flops / s2 / 1e12 / peak, "mfma_peak_tflops": peak,
                            "hbm_gbs": byts / s2 / 1e9, "frac_hbm": byts / s2 / 1e9 / HBM_PEAK_GBS,
                            "active_experts": A}
+            progress(f"{name}: {s2 * 1e3:.3f} ms per layer")
             del host, dev_b
         del pools, tables, runner
         torch.cuda.empty_cache()
     if not args.no_extra and args.only in ("", "mfma"):
         extra["mfma_rate"] = measure_mfma_rate(dev)
+        progress("mfma probe done")
     if not args.no_extra and args.only in ("", "router"):
         extra["router"] = measure_router(dev)
+        progress("router done")
     if not args.no_extra and args.only in ("", "routed"):
         extra["decode_routed_layer"] = measure_routed_layer(dev, gen)
+        progress("routed layer done")
     if not args.no_extra and args.only in ("", "shared"):
         extra["decode_with_shared_expert"] = measure_shared(dev, gen)
+        progress("shared expert done")
     if not args.no_extra and args.only in ("", "offload") and args.offload_steps > 0:
         extra["offload_config4"] = measure_offload(dev, n_steps=args.offload_steps)
+        progress("offload done")
     if extra:
         line["extra"] = extra
     if not args.no_cpu_baseline and args.only == "":
         line["cpu_baseline"] = cpu_baseline()
+        progress("cpu baseline done")
         line["cpu_baseline"]["host_threads_available"] = os.cpu_count()
     if not args.no_cpu_baseline and args.only in ("", "cpu"):
         extra["cpu_baselines"] = cpu_baselines()
+        progress("cpu baselines of configs 0, 2, 3, 4 done")
         if "offload_config4" in extra:  # the CPU leg checks the offload leg's policy too
             extra["offload_config4"]["lru_replay"] = offload_lru_replay(extra["offload_config4"])
         line["extra"] = extra

@@ -76,6 +76,38 @@ int dsv4_mxfp4_dequant_bf16(const void* packed, const void* scales, void* out, i
                     "dequant launch");
 }
 
+int dsv4_mxfp4_dequant_bf16_multi(int n, const void* const* packed, const void* const* scales, void* const* out,
+                                  const int64_t* n_rows, const int64_t* k, void* stream) {
+  REQUIRE(n >= 1 && n <= kDequantMaxJobs, DSV4_ERR_UNSUPPORTED, "dequant multi: %d tensors (1..%d)", n,
+          kDequantMaxJobs);
+  REQUIRE(packed && scales && out && n_rows && k, DSV4_ERR_NULL, "dequant multi: null host array");
+  Dsv4DequantJobs J{};
+  J.n = n;
+  for (int i = 0; i < n; ++i) {
+    REQUIRE(n_rows[i] >= 0 && k[i] >= 0, DSV4_ERR_SHAPE, "dequant multi: tensor %d has a negative size", i);
+    REQUIRE(k[i] % 32 == 0, DSV4_ERR_SHAPE, "dequant multi: tensor %d: K=%lld must be a multiple of 32", i,
+            (long long)k[i]);
+    const uintptr_t pp = (uintptr_t)packed[i];
+    const bool tiled = (pp & DSV4_TILED_WEIGHTS) != 0;  // MFMA-tiled layout, tagged as in dsv4_expert_ptrs
+    const void* src = (const void*)(pp & ~(uintptr_t)DSV4_TILED_WEIGHTS);
+    REQUIRE(!tiled || (n_rows[i] % 16 == 0 && k[i] % 256 == 0), DSV4_ERR_SHAPE,
+            "dequant multi: tensor %d: tiled weights need rows %% 16 == 0 and K %% 256 == 0", i);
+    const int64_t chunks = n_rows[i] * (k[i] / 32);
+    if (chunks > 0) {
+      REQUIRE(src && scales[i] && out[i], DSV4_ERR_NULL, "dequant multi: tensor %d: null pointer", i);
+      REQUIRE(aligned(src, 16) && aligned(out[i], 16), DSV4_ERR_SHAPE,
+              "dequant multi: tensor %d: packed and out need 16-byte alignment", i);
+    }
+    J.packed[i] = (const uint8_t*)src;
+    J.scales[i] = (const uint8_t*)scales[i];
+    J.out[i] = (uint16_t*)out[i];
+    J.kc[i] = k[i] / 32;
+    J.tiled[i] = tiled ? 1 : 0;
+    J.start[i + 1] = J.start[i] + chunks;
+  }
+  return hip_status(launch_mxfp4_dequant_multi(J, (hipStream_t)stream), "dequant multi launch");
+}
+
 int dsv4_mxfp4_tile_weights(const void* src, void* dst, int64_t n_rows, int64_t k, int inverse, void* stream) {
   REQUIRE(n_rows >= 0 && k >= 0, DSV4_ERR_SHAPE, "tile weights: negative size");
   REQUIRE(n_rows % 16 == 0 && k % 256 == 0, DSV4_ERR_SHAPE,
@@ -670,6 +702,14 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
   // concurrent split: h is quantised in the epilogues (no h-quantisation launch
   // between the two GEMMs reads the hot rows), so the hot rows' gate/up and down
   // need nothing from the main stream after the align
+  // Under stream capture the layer keeps one stream: the shared side stream would
+  // join the caller's capture, and another thread's layer on this device could then
+  // put its work into that graph.
+  if (!one_stream && w.hot_min > 0 && hq_fused && hot_concurrent()) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+      one_stream = true;
+  }
   SideStream* side = nullptr;
   std::unique_lock<std::mutex> side_lock;
   if (w.hot_min > 0 && hq_fused && !one_stream && hot_concurrent()) {
@@ -681,19 +721,28 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
     if (rc) return rc;
   }
   const hipStream_t hot_stream = side ? side->s : (hipStream_t)stream;
+  // Once forked, the side stream is joined back into the caller's stream on every
+  // path out, failures included, so the caller's stream still orders all of it.
+  auto join = [&](int status_in) {
+    if (!side) return status_in;
+    int j = hip_status(hipEventRecord(side->join, side->s), "layer: join record");
+    if (!j) j = hip_status(hipStreamWaitEvent((hipStream_t)stream, side->join, 0), "layer: join wait");
+    side = nullptr;
+    return status_in ? status_in : j;
+  };
   if (side) {
     rc = hip_status(launch_moe_gemm_gateup(hot_args(gu), hot_stream), "gemm gate/up (large tiles) launch");
-    if (rc) return rc;
+    if (rc) return join(rc);
   }
   rc = hip_status(launch_moe_gemm_gateup(gu, (hipStream_t)stream), "gemm gate/up launch");
-  if (rc) return rc;
+  if (rc) return join(rc);
   if (w.hot_min > 0 && !side) {
     rc = hip_status(launch_moe_gemm_gateup(hot_args(gu), hot_stream), "gemm gate/up (large tiles) launch");
     if (rc) return rc;
   }
   if (!hq_fused && !pure) {  // FP8 blocks of 128 columns span four single-wave workgroups
     rc = dsv4_fp8_act_quant(base + w.h, Rt, I, 128, nullptr, base + w.ha, nullptr, base + w.hs, stream);
-    if (rc) return rc;
+    if (rc) return join(rc);
   }
   Dsv4GemmArgs dn{};
   dn.afmt = afmt;
@@ -718,15 +767,11 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
   }
   if (w.hot_min > 0) {
     rc = hip_status(launch_moe_gemm_down(hot_args(dn), hot_stream), "gemm down (large tiles) launch");
-    if (rc) return rc;
+    if (rc) return join(rc);
   }
   rc = hip_status(launch_moe_gemm_down(dn, (hipStream_t)stream), "gemm down launch");
+  rc = join(rc);  // the combine reads the hot rows' down outputs
   if (rc) return rc;
-  if (side) {  // the combine reads the hot rows' down outputs
-    rc = hip_status(hipEventRecord(side->join, side->s), "layer: join record");
-    if (!rc) rc = hip_status(hipStreamWaitEvent((hipStream_t)stream, side->join, 0), "layer: join wait");
-    if (rc) return rc;
-  }
   // ids outside [0, E) were skipped by the align (never computed) and add nothing here
   REQUIRE(aligned(y, 16), DSV4_ERR_SHAPE, "layer: y not 16-byte aligned");
   const uint16_t* outp = (const uint16_t*)(base + w.out);
@@ -762,16 +807,21 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
 // device current, and only that address is handed to kernels. The layer needs
 // no zeroed workspace (every region is written before it is read), so nothing
 // is cleared between calls; calls that overlap on one GPU (different streams)
-// share the array and race.
+// share the array and would race, so a call from a stream other than the
+// device's last one is refused unless the caller declares it ordered.
 static constexpr int64_t kScratchBytes = (int64_t)DSV4_NOALLOC_SCRATCH_BYTES;
 static constexpr int kMaxDevices = 64;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[kMaxDevices] = {};
+static void* g_scratch_stream[kMaxDevices] = {};  // stream of the device's last call
+static bool g_scratch_used[kMaxDevices] = {};
 
 // Device address of `scratch` on the device that owns `stream` (looked up on
-// that device's first call; later calls reuse it).
-static int scratch_address(void* stream, void** out) {
+// that device's first call; later calls reuse it). Claims the array for
+// `stream`: DSV4_ERR_STATE if the device's last call came from another stream
+// and `ordered` is false.
+static int scratch_address(void* stream, bool ordered, void** out) {
   int cur = 0;
   hipError_t e = hipGetDevice(&cur);
   if (e != hipSuccess) return hip_status(e, "no-alloc layer: hipGetDevice");
@@ -795,15 +845,24 @@ static int scratch_address(void* stream, void** out) {
     REQUIRE(p && aligned(p, 256), DSV4_ERR_STATE, "no-alloc layer: scratch address not 256-byte aligned");
     g_scratch_ptr[dev] = p;
   }
+  REQUIRE(!g_scratch_used[dev] || g_scratch_stream[dev] == stream || ordered, DSV4_ERR_STATE,
+          "no-alloc layer: device %d's scratch was last used from stream %p, this call comes from %p; calls on "
+          "different streams race unless ordered (synchronize, or wait for an event, then pass "
+          "DSV4_NOALLOC_STREAMS_ORDERED)",
+          (int)dev, g_scratch_stream[dev], stream);
+  g_scratch_used[dev] = true;
+  g_scratch_stream[dev] = stream;
   *out = g_scratch_ptr[dev];
   return DSV4_OK;
 }
 
 int dsv4_moe_layer_forward_noalloc(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
                                    const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
-                                   float swiglu_limit, void* y, void* stream) {
+                                   float swiglu_limit, void* y, int flags, void* stream) {
   REQUIRE(profile == DSV4_PROFILE_BF16 || profile == DSV4_PROFILE_A4W4 || profile == DSV4_PROFILE_BF16_PURE,
           DSV4_ERR_UNSUPPORTED, "no-alloc layer: unknown profile %d", profile);
+  REQUIRE((flags & ~DSV4_NOALLOC_STREAMS_ORDERED) == 0, DSV4_ERR_UNSUPPORTED, "no-alloc layer: unknown flags 0x%x",
+          flags);
   REQUIRE(T >= 0 && K > 0 && K <= DSV4_MAX_TOPK && E > 0 && D > 0 && I > 0, DSV4_ERR_SHAPE,
           "no-alloc layer: bad sizes T=%d K=%d E=%d D=%d I=%d", T, K, E, D, I);
   if (T == 0) return DSV4_OK;
@@ -813,7 +872,7 @@ int dsv4_moe_layer_forward_noalloc(int profile, int scale_rule, const void* x, c
           "or dsv4_moe_layer_forward with a caller workspace)",
           (long long)need, (long long)kScratchBytes);
   void* ws = nullptr;
-  int rc = scratch_address(stream, &ws);
+  int rc = scratch_address(stream, (flags & DSV4_NOALLOC_STREAMS_ORDERED) != 0, &ws);
   if (rc) return rc;
   // one stream: this entry point creates nothing (no side stream or events)
   return layer_forward(profile, scale_rule, x, topk_ids, ids_int64, topk_w, T, K, E, D, I, expert_table, nullptr,

@@ -270,16 +270,15 @@ DSV4_DEV uint32_t pk_bf16(float a, float b) {
 DSV4_DEV float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 DSV4_DEV float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// silu(min(g, L)) * clamp(u, +-L) * w for bf16-rounded g, u; silu(g) = g / (1 + e^-g)
-// from the hardware exp2 and reciprocal (within an fp32 ulp or two of the correctly
-// rounded value, below the bf16 rounding of h that follows)
+// silu(min(g, L)) * clamp(u, +-L) * w for bf16-rounded g, u, with silu(g) = g / (1 + e^-g)
+// written exactly as the 16/64-row kernels' epilogue (expf, IEEE divide), so a token row
+// gets the same h whichever kernel its expert runs on (deepseek_v4.py:184-187)
 DSV4_DEV float big_swiglu(float gt, float up, float w, float limit) {
   if (limit > 0.0f) {
     up = fminf(fmaxf(up, -limit), limit);
     gt = fminf(gt, limit);
   }
-  const float e = __builtin_amdgcn_exp2f(gt * -1.4426950408889634f);
-  return gt * __builtin_amdgcn_rcpf(1.0f + e) * up * w;
+  return gt / (1.0f + expf(-gt)) * up * w;
 }
 
 // 4 E4M3 codes of a * inv .. d * inv (inv = 2^-k), byte 0 = a

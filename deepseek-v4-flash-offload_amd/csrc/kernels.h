@@ -16,6 +16,21 @@ struct Dsv4ExpertPtrs {
 
 hipError_t launch_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, uint16_t* out,
                                 int64_t n_elems, hipStream_t st);
+// Up to kDequantMaxJobs tensors in one launch; start[j] = first 16-byte packed chunk
+// (32 elements) of tensor j in the launch's numbering (start[0] = 0, start[n] = total);
+// kc[j] = K/32 chunks per row; tiled[j]: packed in the MFMA-tiled layout (rows % 16 == 0,
+// K % 256 == 0) instead of the checkpoint layout.
+constexpr int kDequantMaxJobs = 8;
+struct Dsv4DequantJobs {
+  const uint8_t* packed[kDequantMaxJobs];
+  const uint8_t* scales[kDequantMaxJobs];
+  uint16_t* out[kDequantMaxJobs];
+  int64_t start[kDequantMaxJobs + 1];
+  int64_t kc[kDequantMaxJobs];
+  int tiled[kDequantMaxJobs];
+  int n;
+};
+hipError_t launch_mxfp4_dequant_multi(const Dsv4DequantJobs& jobs, hipStream_t st);
 // packed E2M1 weights [N, K/2] <-> the MFMA-tiled layout (inverse = 1: tiled -> natural)
 hipError_t launch_mxfp4_tile(const uint8_t* src, uint8_t* dst, int64_t N, int64_t K, int inverse, hipStream_t st);
 // y[M, N] = bf16(x[M, K] @ dequant(packed, scales)^T), fp32 accumulation, M <= 16

@@ -81,6 +81,73 @@ __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint32_t* __re
   }
 }
 
+// Several tensors in one launch (an expert's w1, w2, w3), each in the checkpoint
+// layout or the MFMA-tiled one (dsv4_mxfp4_tile_weights). One thread per 16-byte
+// packed chunk (32 elements, one E8M0 scale), taken in the SOURCE order so every
+// wave loads one contiguous span; the chunk's 64 output bytes go to their
+// checkpoint-layout place. Tiled chunk t holds packed[16 nt + r][16 (8 j + 2 g + ji)
+// .. +16) with t = ((nt K/256 + j) 2 + ji) 64 + r + 16 g. The tensors' chunks are
+// numbered one after the other (job q holds chunks start[q] .. start[q+1]-1); a chunk
+// finds its tensor by comparing against the starts, unrolled, so the argument
+// arrays are only indexed by constants.
+constexpr int kDequantChunksPerThread = 2;
+
+__global__ __launch_bounds__(256) void mxfp4_dequant_multi_kernel(Dsv4DequantJobs J) {
+  const int64_t total = J.start[J.n];
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  const int64_t c0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  u32x4 p[kDequantChunksPerThread];
+  uint32_t s[kDequantChunksPerThread];
+  u32x4* o[kDequantChunksPerThread];
+#pragma unroll
+  for (int i = 0; i < kDequantChunksPerThread; ++i) {
+    const int64_t c = c0 + i * stride;
+    o[i] = nullptr;
+    if (c < total) {
+      int q = 0;
+#pragma unroll
+      for (int j = 1; j < kDequantMaxJobs; ++j)
+        if (j < J.n && c >= J.start[j]) q = j;
+      const uint8_t* pk = J.packed[0];
+      const uint8_t* sc = J.scales[0];
+      uint16_t* ot = J.out[0];
+      int64_t kc = J.kc[0];
+      int tl = J.tiled[0];
+      int64_t t = c - J.start[0];
+#pragma unroll
+      for (int j = 1; j < kDequantMaxJobs; ++j)
+        if (j == q) {
+          pk = J.packed[j];
+          sc = J.scales[j];
+          ot = J.out[j];
+          kc = J.kc[j];
+          tl = J.tiled[j];
+          t = c - J.start[j];
+        }
+      int64_t nat = t;  // checkpoint-layout chunk index n * K/32 + cb
+      if (tl) {
+        const int L = (int)(t & 63);
+        const int64_t qq = t >> 6;
+        const int ji = (int)(qq & 1);
+        const int64_t nst = kc >> 3;
+        const int64_t j = (qq >> 1) % nst, nt = (qq >> 1) / nst;
+        nat = (16 * nt + (L & 15)) * kc + 8 * j + 2 * (L >> 4) + ji;
+      }
+      p[i] = __builtin_nontemporal_load((const u32x4*)pk + t);
+      s[i] = sc[nat];
+      o[i] = (u32x4*)ot + 4 * nat;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kDequantChunksPerThread; ++i)
+    if (o[i]) {
+      __builtin_nontemporal_store(dequant8(p[i].x, s[i]), o[i]);
+      __builtin_nontemporal_store(dequant8(p[i].y, s[i]), o[i] + 1);
+      __builtin_nontemporal_store(dequant8(p[i].z, s[i]), o[i] + 2);
+      __builtin_nontemporal_store(dequant8(p[i].w, s[i]), o[i] + 3);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Activation quantisers (bodies in quant_dev.h): one thread per 8-element group.
 // ---------------------------------------------------------------------------
@@ -263,6 +330,17 @@ hipError_t launch_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, ui
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   hipLaunchKernelGGL(mxfp4_dequant_kernel, dim3((unsigned)grid), dim3(256), 0, st,
                      (const uint32_t*)packed, scales, (u32x4*)out, n_groups);
+  return hipGetLastError();
+}
+
+hipError_t launch_mxfp4_dequant_multi(const Dsv4DequantJobs& jobs, hipStream_t st) {
+  if (jobs.n < 1 || jobs.n > kDequantMaxJobs) return hipErrorInvalidValue;
+  const int64_t n_chunks = jobs.start[jobs.n];
+  if (n_chunks == 0) return hipSuccess;
+  const int64_t per_wg = 256LL * kDequantChunksPerThread;
+  const int64_t grid = (n_chunks + per_wg - 1) / per_wg;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(mxfp4_dequant_multi_kernel, dim3((unsigned)grid), dim3(256), 0, st, jobs);
   return hipGetLastError();
 }
 

@@ -26,6 +26,7 @@ MAX_EXPERTS = 512
 MAX_TOPK = 32
 UNPERMUTE_MAX_ROWS = 64  # rows one token may receive in moe_unpermute
 NOALLOC_SCRATCH_BYTES = 64 << 20  # static workspace of dsv4_moe_layer_forward_noalloc
+NOALLOC_STREAMS_ORDERED = 1  # its flag: this call is ordered after every earlier one on the device
 TILED_WEIGHTS = 1  # pointer tag of an MFMA-tiled packed field in the expert table
 
 _c_p = ctypes.c_void_p
@@ -38,6 +39,8 @@ SIGNATURES = {
     "dsv4_last_error": (ctypes.c_char_p, []),
     "dsv4_abi_version": (_i32, []),
     "dsv4_mxfp4_dequant_bf16": (_i32, [_c_p, _c_p, _c_p, _i64, _i64, _c_p]),
+    "dsv4_mxfp4_dequant_bf16_multi": (_i32, [_i32, ctypes.POINTER(_c_p), ctypes.POINTER(_c_p), ctypes.POINTER(_c_p),
+                                             ctypes.POINTER(_i64), ctypes.POINTER(_i64), _c_p]),
     "dsv4_mxfp4_gemv_bf16": (_i32, [_c_p, _i32, _c_p, _c_p, _i32, _i32, _c_p, _c_p]),
     "dsv4_mxfp4_tile_weights": (_i32, [_c_p, _c_p, _i64, _i64, _i32, _c_p]),
     "dsv4_mxfp4_tile_host": (_i32, [_c_p, _c_p, _i64, _i64]),
@@ -63,7 +66,7 @@ SIGNATURES = {
     "dsv4_moe_layer_forward": (_i32, [_i32, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32, _c_p,
                                       _f32, _c_p, _i64, _c_p, _c_p]),
     "dsv4_moe_layer_forward_noalloc": (_i32, [_i32, _i32, _c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32,
-                                              _c_p, _f32, _c_p, _c_p]),
+                                              _c_p, _f32, _c_p, _i32, _c_p]),
     "dsv4_moe_layer_shared_workspace_bytes": (_i32, [_i32, _i32, _i32, _i32, _i32, ctypes.POINTER(_i64)]),
     "dsv4_moe_layer_forward_shared": (_i32, [_c_p, _c_p, _i32, _c_p, _i32, _i32, _i32, _i32, _i32, _c_p] + [_c_p] * 6
                                       + [_f32, _c_p, _i64, _c_p, _c_p]),
@@ -94,6 +97,9 @@ SIGNATURES = {
     "dsv4_probe_mfma_rate": (_i32, [_i32, _i32, _i32, _i32, _i32, _c_p, _c_p, _c_p]),
 }
 
+# DSV4_ABI_VERSION of include/dsv4_moe.h that SIGNATURES above describe
+ABI_VERSION = 2
+
 _LIB = None
 
 
@@ -118,8 +124,9 @@ def lib():
             fn = getattr(h, name)
             fn.restype = res
             fn.argtypes = args
-        if h.dsv4_abi_version() != 1:
-            raise RuntimeError("libdsv4hip.so ABI version mismatch")
+        got = h.dsv4_abi_version()
+        if got != ABI_VERSION:
+            raise RuntimeError(f"libdsv4hip.so ABI version {got}, this binding expects {ABI_VERSION}")
         _LIB = h
     return _LIB
 

@@ -62,6 +62,33 @@ def dequant_mxfp4(w_packed: torch.Tensor, scale: torch.Tensor, out: Optional[tor
     return out
 
 
+def dequant_mxfp4_multi(pairs, tiled: bool = False):
+    """Several ``(packed [N, K/2], scale [N, K/32])`` pairs -> a list of bf16 ``[N, K]``
+    tensors in ONE launch (bit-exact, as ``dequant_mxfp4``): an expert's w1, w2, w3.
+    ``tiled``: the packed bytes are in the MFMA-tiled layout (``tile_weights``), as
+    the slot records store them; the outputs are the checkpoint layout either way."""
+    pairs = list(pairs)
+    n = len(pairs)
+    if not 1 <= n <= 8:
+        raise ValueError(f"dequant_mxfp4_multi: {n} tensors (1..8)")
+    wps, scs, outs = [], [], []
+    for w_packed, scale in pairs:
+        _dev(w_packed, "dequant_mxfp4_multi")
+        wp, sc = _u8(w_packed), _u8(scale)
+        if wp.dim() != 2 or sc.shape != (wp.shape[0], wp.shape[1] // 16):
+            raise ValueError(f"scale shape {tuple(sc.shape)} does not match packed {tuple(wp.shape)}")
+        wps.append(wp)
+        scs.append(sc)
+        outs.append(torch.empty((wp.shape[0], 2 * wp.shape[1]), dtype=torch.bfloat16, device=wp.device))
+    arr = ctypes.c_void_p * n
+    i64 = ctypes.c_int64 * n
+    tag = _lib.TILED_WEIGHTS if tiled else 0
+    call("dsv4_mxfp4_dequant_bf16_multi", n, arr(*[t.data_ptr() | tag for t in wps]), arr(*[t.data_ptr() for t in scs]),
+         arr(*[t.data_ptr() for t in outs]), i64(*[t.shape[0] for t in wps]), i64(*[2 * t.shape[1] for t in wps]),
+         _stream(wps[0]))
+    return outs
+
+
 def mxfp4_gemv(x: torch.Tensor, w_packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     """``bf16(x @ dequant(W)^T)`` for up to 16 bf16 rows of x, fp32 accumulation."""
     _dev(x, "mxfp4_gemv")

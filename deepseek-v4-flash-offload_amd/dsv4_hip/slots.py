@@ -176,6 +176,16 @@ class SlotCache:
     def copy_record(self, layer, eid, dst):
         call("dsv4_slots_copy_record", self.h, int(layer), int(eid), ctypes.c_void_p(dst.data_ptr()), self._stream())
 
+    def record_bytes_views(self, buf):
+        """The fields of a record copied into ``buf`` as uint8 views in the registered
+        shapes, packed fields in the stored layout (MFMA-tiled when ``layout.tiled``)."""
+        out = {}
+        for k in FIELDS:
+            o = self.layout.offsets[k]
+            N = self.layout.shapes[k][0]
+            out[k] = buf[o:o + self.layout.nbytes[k]].view(N, -1)
+        return out
+
     def record_views(self, buf):
         """The fields of a record copied into ``buf``, as registered (see slot_views)."""
         out = {}

@@ -241,9 +241,16 @@ class OffloadDeepseekV4MoE(_BASE):
         evicting). The experts are acquired ``cap`` at a time; each part runs the
         grouped GEMMs on the routed rows of its experts (the other ids are masked
         out of its layout) into one buffer of per-row outputs, and a single combine
-        sums every token's rows in ascending expert id, so the result equals the
-        one-part layer bit for bit. With a fused shared expert, its output (the
-        layer with no routed rows) is added as forward adds the shared MLP's."""
+        sums every token's rows in ascending expert id. Each part takes the M-block
+        size the one-part layer takes (16-row blocks below 2048 routed rows, 64 from
+        there) with h quantised by its own launch, which the one-part layer's fused
+        epilogue matches bit for bit, so the result equals the one-part layer bit for
+        bit, except where the one-part layer sends its hot experts to the large-tile
+        kernel (from 16,384 routed rows): there the bf16 profile's FP8 x FP4 MFMAs
+        group the products of a sum differently and the two agree within the GEMM
+        parity bar (the a4w4 products and partial sums are exact, so a4w4 stays bit
+        for bit). With a fused shared expert, its output (the layer with no routed
+        rows) is added as forward adds the shared MLP's."""
         T, D = x.shape
         K = indices.shape[1]
         E = self.n_routed_experts
@@ -261,6 +268,8 @@ class OffloadDeepseekV4MoE(_BASE):
         else:
             xa, xs, _ = _ops.mxfp4_act_quant(x, rule)
             afmt = _lib.AFMT_E2M1
+        # the one-part layer's M-block size (layer_block_m in csrc/capi.cpp)
+        bm = 64 if T * K >= 2048 else _lib.GEMM_BLOCK_M
         out = None
         h = None
         for i in range(0, uniq.size, cap):
@@ -271,7 +280,7 @@ class OffloadDeepseekV4MoE(_BASE):
                 out = torch.empty((T * K, D), dtype=torch.bfloat16, device=x.device)
                 h = torch.empty((T * K, inter), dtype=torch.bfloat16, device=x.device)
             keep = torch.isin(ids, torch.from_numpy(part.astype(np.int32)).to(x.device))
-            al = _ops.moe_align(torch.where(keep, ids, torch.full_like(ids, -1)), None, E)
+            al = _ops.moe_align(torch.where(keep, ids, torch.full_like(ids, -1)), None, E, block_m=bm)
             _ops.gemm_gateup(afmt, xa, xs, K, al, table, D, inter, w, limit, out=h)
             if fp8:
                 q = _ops.fp8_act_quant(h, 128, want_codes=True, want_e8m0x4=True)

@@ -105,14 +105,14 @@ class ExpertBank:
 
     # -- device bf16 cache (reference get) ----------------------------------
     def _dequant_on_device(self, layer, eid):
+        """One record copy and ONE dequant launch for the expert's three tensors (the
+        reference dequantises them one call each, ``offload.py:77-84``)."""
         buf = torch.empty(self._layout.record_bytes, dtype=torch.uint8, device=self.device)
         self._slots.copy_record(layer, eid, buf)
-        v = self._slots.record_views(buf)
-        out = {}
-        for w in ("w1", "w2", "w3"):
-            t = ops.dequant_mxfp4(v[w + "p"], v[w + "s"])
-            out[w] = t if self.dtype == torch.bfloat16 else t.to(self.dtype)
-        return out
+        v = self._slots.record_bytes_views(buf)   # packed fields as stored (tiled or not)
+        names = ("w1", "w2", "w3")
+        ts = ops.dequant_mxfp4_multi([(v[w + "p"], v[w + "s"]) for w in names], tiled=self._layout.tiled)
+        return {w: (t if self.dtype == torch.bfloat16 else t.to(self.dtype)) for w, t in zip(names, ts)}
 
     def get(self, layer, eid):
         self._need_gpu("get")

@@ -21,11 +21,15 @@
 extern "C" {
 #endif
 
-#define DSV4_ABI_VERSION 1
+/* 2: dsv4_moe_unpermute gained `status_out` (before `stream`), dsv4_slots_invalidate
+ *    gained `compute_stream`, dsv4_moe_layer_forward_noalloc gained `flags` (before
+ *    `stream`), GEMM reduction lengths stop at 4096 (8192 dropped).
+ *    Callers built against version 1 must not call a version-2 library. */
+#define DSV4_ABI_VERSION 2
 
 #define DSV4_MAX_EXPERTS 512
 #define DSV4_MAX_TOPK 32
-#define DSV4_GEMM_BLOCK_M 16 /* rows per M block for decode-sized calls; the GEMMs also take 64 and 128 */
+#define DSV4_GEMM_BLOCK_M 16 /* rows per M block for decode-sized calls; the GEMMs also take 64, 128 and 256 */
 
 /* activation formats of the grouped GEMM A operand */
 #define DSV4_AFMT_E4M3 0 /* one E4M3fn code per byte, E8M0 per 32 (bf16 profile) */
@@ -73,6 +77,19 @@ int dsv4_abi_version(void);
  * packed [n_rows, k/2], scales [n_rows, k/32], out [n_rows, k]; k % 32 == 0. */
 int dsv4_mxfp4_dequant_bf16(const void* packed, const void* scales, void* out, int64_t n_rows, int64_t k,
                             void* stream);
+
+/* Up to 8 MXFP4 weights -> bf16 in one launch, each bit-exact as
+ * dsv4_mxfp4_dequant_bf16. Replaces the three npu_ops.dequant_fp4_weight calls
+ * with which the reference's ExpertBank.get fills a bf16 expert
+ * (offload.py:77-84): w1, w2 and w3 of one expert in one call. `packed`,
+ * `scales`, `out`, `n_rows` and `k` are host arrays of `n` (1..8) entries:
+ * packed[i] [n_rows[i], k[i]/2], scales[i] [n_rows[i], k[i]/32], out[i]
+ * [n_rows[i], k[i]] (device pointers, packed and out 16-byte aligned);
+ * k[i] % 32 == 0. A packed pointer with DSV4_TILED_WEIGHTS set is read in the
+ * MFMA-tiled layout (n_rows % 16 == 0, k % 256 == 0), as the slot records hold
+ * it; the output is the checkpoint layout either way. */
+int dsv4_mxfp4_dequant_bf16_multi(int n, const void* const* packed, const void* const* scales, void* const* out,
+                                  const int64_t* n_rows, const int64_t* k, void* stream);
 
 /* Packed E2M1 weights [n_rows, k/2] (checkpoint layout, npu_ops.py:142-158) to the
  * MFMA-tiled layout the grouped GEMMs stream fastest, or back (inverse = 1):
@@ -195,7 +212,10 @@ int dsv4_moe_combine(const void* out_flat, const void* topk_ids, int ids_int64, 
  * [rows, D/2] (E2M1), a_scale [rows, D/32]. h_out: bf16 [R, I] by flat index.
  * block_m (the moe_align block size) is 16 (single-wave workgroups, decode),
  * 64 or 128 (LDS-tiled workgroups: each weight fragment serves 4 or 8 row
- * tiles); D and I must be 256 * 2^n (512..4096) and I a multiple of 128. */
+ * tiles) or 256 (large-tile workgroups, 32x32x64 MFMAs, E4M3/E2M1 A only: D a
+ * multiple of 1024 for gate/up, I of 1024 and D of 256 for down); D and I must
+ * be 256 * 2^n (512..4096) and I a multiple of 128. The bf16 A format takes
+ * block_m 16 or 64. */
 int dsv4_moe_gemm_gateup(int afmt, const void* a, const void* a_scale, int a_row_div, const int32_t* sorted_ids,
                          const int32_t* block_expert, const int32_t* num_post_padded, int R, int block_m,
                          int max_blocks, const void* expert_table, int D, int I, const float* topk_w,
@@ -234,13 +254,20 @@ int dsv4_moe_layer_forward(int profile, int scale_rule, const void* x, const voi
  * DSV4_NOALLOC_SCRATCH_BYTES (64 MiB) that each GPU the library runs on holds
  * until the process ends; a call whose dsv4_moe_layer_workspace_bytes exceeds
  * it returns DSV4_ERR_UNSUPPORTED (about 500 tokens at top-8, hidden 4096,
- * inter 2048). The array is per device and shared by every call on it: calls
- * that overlap on one GPU (on different streams) race. Outputs equal
- * dsv4_moe_layer_forward's bit for bit. */
+ * inter 2048). The array is per device and shared by every call on it, and
+ * keeps the last call's contents. Calls on one stream are ordered by it; calls
+ * that overlap on one GPU (different streams, not ordered by the caller) race.
+ * The library remembers the stream of each device's last call and rejects
+ * (DSV4_ERR_STATE, before anything is enqueued) a call from another stream
+ * unless `flags` holds DSV4_NOALLOC_STREAMS_ORDERED: the caller's promise that
+ * this call is ordered after every earlier call on the device (a synchronize,
+ * or an event the new stream waits for). Outputs equal dsv4_moe_layer_forward's
+ * bit for bit. */
 #define DSV4_NOALLOC_SCRATCH_BYTES (64 << 20)
+#define DSV4_NOALLOC_STREAMS_ORDERED 1
 int dsv4_moe_layer_forward_noalloc(int profile, int scale_rule, const void* x, const void* topk_ids, int ids_int64,
                                    const float* topk_w, int T, int K, int E, int D, int I, const void* expert_table,
-                                   float swiglu_limit, void* y, void* stream);
+                                   float swiglu_limit, void* y, int flags, void* stream);
 
 /* The same layer with the shared expert folded in as one more group of the
  * grouped GEMMs (bf16 profile): OffloadDeepseekV4MoE.forward's

@@ -32,7 +32,8 @@ def test_python_binding_covers_header():
 
 
 def test_abi_version():
-    assert _lib.lib().dsv4_abi_version() == 1
+    m = re.search(r"#define DSV4_ABI_VERSION (\d+)", open(HEADER).read())
+    assert m and int(m.group(1)) == _lib.ABI_VERSION == _lib.lib().dsv4_abi_version()
 
 
 def _err(rc):
@@ -46,6 +47,26 @@ def test_dequant_validation():
     rc, msg = _err(lib.dsv4_mxfp4_dequant_bf16(None, None, None, 4, 64, None))
     assert rc == -1 and "null" in msg
     assert lib.dsv4_mxfp4_dequant_bf16(None, None, None, 0, 64, None) == 0  # empty is a no-op
+
+
+def test_dequant_multi_validation():
+    lib = _lib.lib()
+    P = ctypes.c_void_p * 2
+    L = ctypes.c_int64 * 2
+    nul = P(None, None)
+    rc, msg = _err(lib.dsv4_mxfp4_dequant_bf16_multi(0, nul, nul, nul, L(1, 1), L(32, 32), None))
+    assert rc == -3 and "tensors" in msg
+    rc, msg = _err(lib.dsv4_mxfp4_dequant_bf16_multi(9, nul, nul, nul, L(1, 1), L(32, 32), None))
+    assert rc == -3
+    rc, msg = _err(lib.dsv4_mxfp4_dequant_bf16_multi(2, nul, nul, nul, L(0, 1), L(32, 48), None))
+    assert rc == -2 and "multiple of 32" in msg
+    rc, msg = _err(lib.dsv4_mxfp4_dequant_bf16_multi(2, nul, nul, nul, L(1, 1), L(32, 32), None))
+    assert rc == -1 and "null" in msg
+    # a tiled source (pointer tag 1) needs 16-row tiles and 256-wide K stages
+    rc, msg = _err(lib.dsv4_mxfp4_dequant_bf16_multi(1, P(1, None), nul, nul, L(8, 0), L(256, 0), None))
+    assert rc == -2 and "tiled" in msg
+    # empty tensors are no-ops, null pointers allowed for them
+    assert lib.dsv4_mxfp4_dequant_bf16_multi(2, nul, nul, nul, L(0, 4), L(64, 0), None) == 0
 
 
 def test_quant_validation():

@@ -20,7 +20,7 @@ last routed row of every M block of the 16 hottest experts (the block edges of
 every hot expert; ~260 tokens) plus 32 random ones; at 16384 tokens the same for
 the 8 hottest experts in their 256-row blocks; at 64 tokens, all of them.
 Tolerances: max relative error (normwise) 1e-2 for bf16 and pure bf16, 2e-2 for
-a4w4; per element, bf16 within 5e-2 and pure bf16 within 2e-2 of
+a4w4; per element, bf16 within 3e-2 and pure bf16 within 2e-2 of
 max(|ref|, rms(ref)), a4w4 bit for bit."""
 
 import numpy as np
@@ -37,7 +37,7 @@ pytestmark = pytest.mark.gpu
 E, K, D, I = 256, 8, 4096, 2048
 TOL = {"bf16": 1e-2, "a4w4": 2e-2, "bf16_pure": 1e-2}
 # per element, floor rms(ref) (_parity.elementwise_rel); a4w4 exact
-ELEM_TOL = {"bf16": 5e-2, "a4w4": 0.0, "bf16_pure": 2e-2}
+ELEM_TOL = {"bf16": 3e-2, "a4w4": 0.0, "bf16_pure": 2e-2}
 
 
 def _bits(t):

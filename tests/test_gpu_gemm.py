@@ -12,7 +12,7 @@ output within one bf16 ulp plus 2^-10 of its sum of absolute products (the
 MFMA drops products far below the largest of their group), the gate/up
 GEMM's h within one ulp plus that bound carried through SwiGLU from its gate
 and up values. The end-to-end tests start from the same bf16 x and routing:
-a4w4 bit for bit; bf16 per element within 5e-2 of max(|ref|, rms(ref)).
+a4w4 bit for bit; bf16 per element within 3e-2 of max(|ref|, rms(ref)).
 """
 
 import numpy as np
@@ -30,7 +30,7 @@ pytestmark = pytest.mark.gpu
 TOL = {"bf16": 1e-2, "a4w4": 2e-2, "bf16_pure": 1e-2}
 # per-element relative error with a floor of rms(output) (_parity.elementwise_rel); a4w4: bit for bit;
 # the pure-bf16 variant has no quantisation step for a 1-ulp difference to move
-ELEM_TOL = {"bf16": 5e-2, "a4w4": 0.0, "bf16_pure": 2e-2}
+ELEM_TOL = {"bf16": 3e-2, "a4w4": 0.0, "bf16_pure": 2e-2}
 
 
 def rel(a, b):
@@ -74,7 +74,19 @@ def _case(T, K, E, D, I, seed, dev):
                                           (640, 8, 8, 4096, 2048, 256)])
 def test_grouped_gemm_stages(gpu, profile, T, K, E, D, I, bm):
     # bm 16 runs the single-wave decode kernel, 64/128 the LDS-tiled kernel, 256 the
-    # large-tile kernel (256 x 256 workgroup tiles, 32x32x64 MFMA)
+    # large-tile kernel (256 x 256 workgroup tiles, 32x32x64 MFMA) in half-block
+    # workgroups (E4M3 always, E2M1 below 32,768 routed rows)
+    _stage_case(gpu, profile, T, K, E, D, I, bm)
+
+
+def test_grouped_gemm_stages_whole_blocks_a4w4(gpu):
+    # from 32,768 routed rows the E2M1 large-tile kernel runs one 8-wave workgroup
+    # per whole 256-row block (csrc/gemm_big.hip launch_moe_gemm_big); every element
+    # of both stages against the oracle, the down GEMM bit for bit
+    _stage_case(gpu, "a4w4", 4096, 8, 16, 1024, 1024, 256)
+
+
+def _stage_case(gpu, profile, T, K, E, D, I, bm):
     ids, w, xb, host, devw, table = _case(T, K, E, D, I, 31 + T, gpu)
     al = ops.moe_align(_dev(ids, gpu), _dev(w, gpu), E, bm)
     R = T * K

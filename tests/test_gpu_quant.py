@@ -50,6 +50,49 @@ def test_dequant_shapes_and_tails(gpu, n, k):
     assert np.array_equal(_bits(out), Q.dequant_fp4_weight(packed, scales))
 
 
+@pytest.mark.parametrize("tiled", [False, True])
+def test_dequant_multi_one_launch_equals_each_tensor(gpu, tiled):
+    # one launch for several tensors (an expert's w1, w2, w3 at the config-1 shapes,
+    # plus odd shapes and an empty one), checkpoint or MFMA-tiled source layout: each
+    # output bit for bit the oracle's dequant of that tensor
+    rng = np.random.default_rng(21 + int(tiled))
+    shapes = [(2048, 4096), (4096, 2048), (2048, 4096), (16, 256), (0, 512), (48, 1024)]
+    if not tiled:
+        shapes += [(3, 96), (1, 32)]
+    host = [(rng.integers(0, 256, (n, k // 2), dtype=np.uint8), rng.integers(0, 256, (n, k // 32), dtype=np.uint8))
+            for n, k in shapes]
+    pairs = []
+    for p_, s_ in host:
+        pt = _u8(p_, gpu)
+        if tiled and p_.size:
+            pt = ops.tile_weights(pt)
+        pairs.append((pt, _u8(s_, gpu)))
+    outs = ops.dequant_mxfp4_multi(pairs, tiled=tiled)
+    torch.cuda.synchronize()
+    for (p_, s_), o in zip(host, outs):
+        assert tuple(o.shape) == (p_.shape[0], 2 * p_.shape[1])
+        assert np.array_equal(_bits(o), Q.dequant_fp4_weight(p_, s_)), p_.shape
+
+
+def test_expert_bank_get_miss_is_one_dequant_launch(gpu, monkeypatch):
+    # offload.py:77-84: the bf16 get of a missing expert (one record copy, one dequant
+    # launch for w1, w2, w3 read from the MFMA-tiled record) equals the oracle bit for bit
+    from offload import ExpertBank
+    calls = []
+    real = ops.dequant_mxfp4_multi
+    monkeypatch.setattr(ops, "dequant_mxfp4_multi", lambda *a, **k: calls.append(1) or real(*a, **k))
+    monkeypatch.setenv("DSV4_PACKED_SLOTS", "2")
+    bank = ExpertBank(capacity=1, device="cuda:0")
+    w = synth.expert_weights(3, 1024, 512)
+    bank.register(0, 3, *(torch.from_numpy(w[k]) for k in ("w1p", "w1s", "w2p", "w2s", "w3p", "w3s")))
+    assert bank._layout.tiled
+    d = bank.get(0, 3)
+    torch.cuda.synchronize()
+    assert len(calls) == 1
+    for nm in ("w1", "w2", "w3"):
+        assert np.array_equal(_bits(d[nm]), Q.dequant_fp4_weight(w[nm + "p"], w[nm + "s"])), nm
+
+
 def _all_finite_bf16_rows(cols):
     b = np.arange(65536, dtype=np.uint32).astype(np.uint16)
     v = Q.bf16_bits_to_f32(b)

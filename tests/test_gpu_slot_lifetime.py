@@ -7,7 +7,10 @@
   ``.to(device)`` copies it cached): a later acquire that reuses the slot does
   not change them.
 * A layer that routes to more experts than the packed slot cache holds runs in
-  parts and gives the same output, bit for bit, as the one-part layer.
+  parts and gives the same output, bit for bit, as the one-part layer; at
+  2048 routed rows and more (64-row blocks) as well, and from 16,384 routed
+  rows, where the one-part layer runs its hot experts on the large-tile kernel,
+  bit for bit in a4w4 and within the GEMM bar in the bf16 profile.
 """
 
 import types
@@ -154,3 +157,36 @@ def test_layer_with_more_routed_experts_than_slots_runs_in_parts(gpu, monkeypatc
     err = float(np.abs(got - want).max() / np.abs(want).max())
     print(f"parts profile={profile} rel_err={err:.3e}")
     assert err <= tol
+
+
+@pytest.mark.parametrize("T,profile", [(256, "bf16"), (256, "a4w4"), (2048, "bf16"), (2048, "a4w4")])
+def test_prefill_sized_layer_in_parts_matches_one_part(gpu, monkeypatch, T, profile):
+    """2048 routed rows (64-row blocks) and 16,384 (the one-part layer splits its
+    hot experts onto the large-tile kernel; hidden and inter 1024 allow it)."""
+    E, K, D, I, layer = 32, 8, 1024, 1024, 6
+    host = {e: synth.expert_weights(e, D, I) for e in range(E)}
+    monkeypatch.setattr(mod, "_MXFP4_GMM", profile == "a4w4")
+    monkeypatch.setattr(mod, "_FUSE_SHARED", False)
+    monkeypatch.setattr(mod, "_FUSED_ROUTE", False)
+    x = (synth.bf16_normal(np.random.default_rng(9), (T, D)).float() * 0.5).to(torch.bfloat16).to(gpu)
+    small = _engine(monkeypatch, 7, E, D, I, layer, host)
+    big = _engine(monkeypatch, 64, E, D, I, layer, host)
+    m_small, m_big = _plugin(small, E, K, layer, D), _plugin(big, E, K, layer, D)
+    _, idx = m_small._route(x, None)
+    counts = np.bincount(idx.cpu().numpy().reshape(-1), minlength=E)
+    print(f"parts T={T} profile={profile}: {int((counts > 0).sum())} experts, max rows {int(counts.max())}",
+          flush=True)
+    y_small = m_small.forward(x)
+    y_big = m_big.forward(x)
+    torch.cuda.synchronize()
+    a = y_small.float().cpu().numpy()
+    b = y_big.float().cpu().numpy()
+    assert np.isfinite(a).all() and np.isfinite(b).all()
+    if profile == "a4w4" or T * K < 16384:
+        assert np.array_equal(y_small.cpu().view(torch.int16).numpy(), y_big.cpu().view(torch.int16).numpy())
+    else:
+        assert (counts >= 128).any()                 # the one-part layer does split
+        ref = np.maximum(np.abs(b), np.sqrt(np.mean(b * b)))
+        worst = float((np.abs(a - b) / ref).max())
+        print(f"parts vs one part (bf16, split) worst {worst:.3e}")
+        assert worst <= 3e-2
