@@ -27,6 +27,7 @@ struct Dsv4DequantJobs {
   uint16_t* out[kDequantMaxJobs];
   int64_t start[kDequantMaxJobs + 1];
   int64_t kc[kDequantMaxJobs];
+  int64_t wg_start[kDequantMaxJobs];  // first workgroup of tensor j (set by the launcher)
   int tiled[kDequantMaxJobs];
   int n;
 };

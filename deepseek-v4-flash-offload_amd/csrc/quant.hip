@@ -82,70 +82,77 @@ __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint32_t* __re
 }
 
 // Several tensors in one launch (an expert's w1, w2, w3), each in the checkpoint
-// layout or the MFMA-tiled one (dsv4_mxfp4_tile_weights). One thread per 16-byte
-// packed chunk (32 elements, one E8M0 scale), taken in the SOURCE order so every
-// wave loads one contiguous span; the chunk's 64 output bytes go to their
-// checkpoint-layout place. Tiled chunk t holds packed[16 nt + r][16 (8 j + 2 g + ji)
-// .. +16) with t = ((nt K/256 + j) 2 + ji) 64 + r + 16 g. The tensors' chunks are
-// numbered one after the other (job q holds chunks start[q] .. start[q+1]-1); a chunk
-// finds its tensor by comparing against the starts, unrolled, so the argument
-// arrays are only indexed by constants.
-constexpr int kDequantChunksPerThread = 2;
-
+// layout or the MFMA-tiled one (dsv4_mxfp4_tile_weights). A workgroup takes 256
+// consecutive 16-byte packed chunks (32 elements, one E8M0 scale each) of one
+// tensor in SOURCE order - one contiguous 4 KB load - and dequantises each into its
+// 64 output bytes in LDS, placed so that the 16 KB then leave in whole contiguous
+// runs: a checkpoint-layout source maps to 16 KB of contiguous output; a tiled one
+// to two 16-row x 256-k units, each 16 row segments of 512 bytes. (Writing each
+// chunk's 64 bytes straight from its lane scatters 16-byte pieces over 16 rows per
+// store instruction: measured at 0.6 TB/s.) Tiled chunk c of a tensor holds
+// packed[16 nt + r][16 (8 j + 2 g + ji) .. +16) with c = ((nt K/256 + j) 2 + ji) 64 +
+// r + 16 g. Workgroup w belongs to the last job q with wg_start[q] <= w (uniform).
 __global__ __launch_bounds__(256) void mxfp4_dequant_multi_kernel(Dsv4DequantJobs J) {
-  const int64_t total = J.start[J.n];
-  const int64_t stride = (int64_t)gridDim.x * 256;
-  const int64_t c0 = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  u32x4 p[kDequantChunksPerThread];
-  uint32_t s[kDequantChunksPerThread];
-  u32x4* o[kDequantChunksPerThread];
+  __shared__ __attribute__((aligned(16))) u32x4 buf[256 * 4];  // 16 KB of bf16 output
+  const int t = threadIdx.x;
+  int q = 0;
 #pragma unroll
-  for (int i = 0; i < kDequantChunksPerThread; ++i) {
-    const int64_t c = c0 + i * stride;
-    o[i] = nullptr;
-    if (c < total) {
-      int q = 0;
+  for (int jb = 1; jb < kDequantMaxJobs; ++jb)
+    if (jb < J.n && (int64_t)blockIdx.x >= J.wg_start[jb]) q = jb;
+  const uint8_t* pk = J.packed[0];
+  const uint8_t* sc = J.scales[0];
+  uint16_t* ot = J.out[0];
+  int64_t kc = J.kc[0], nchunks = J.start[1] - J.start[0], wg0 = J.wg_start[0];
+  int tl = J.tiled[0];
 #pragma unroll
-      for (int j = 1; j < kDequantMaxJobs; ++j)
-        if (j < J.n && c >= J.start[j]) q = j;
-      const uint8_t* pk = J.packed[0];
-      const uint8_t* sc = J.scales[0];
-      uint16_t* ot = J.out[0];
-      int64_t kc = J.kc[0];
-      int tl = J.tiled[0];
-      int64_t t = c - J.start[0];
+  for (int jb = 1; jb < kDequantMaxJobs; ++jb)
+    if (jb == q) {
+      pk = J.packed[jb];
+      sc = J.scales[jb];
+      ot = J.out[jb];
+      kc = J.kc[jb];
+      nchunks = J.start[jb + 1] - J.start[jb];
+      wg0 = J.wg_start[jb];
+      tl = J.tiled[jb];
+    }
+  const int64_t c0 = ((int64_t)blockIdx.x - wg0) * 256;  // first chunk of this workgroup
+  const int64_t c = c0 + t;
+  const int64_t nst = kc >> 3;  // 256-k stages per row (tiled sources)
+  if (c < nchunks) {
+    int64_t nat = c;  // checkpoint-layout chunk index n * K/32 + cb
+    int lpos = 4 * t;  // u32x4 slot of the chunk's first 16 output bytes in buf
+    if (tl) {
+      const int L = (int)(c & 63), ji = (int)((c >> 6) & 1);
+      const int64_t u = c >> 7;  // 16-row x 256-k unit = nt * nst + j
+      const int r = L & 15, cb8 = 2 * (L >> 4) + ji;
+      nat = (16 * (u / nst) + r) * kc + 8 * (u % nst) + cb8;
+      lpos = ((t >> 7) * 512 + r * 32 + cb8 * 4);
+    }
+    const u32x4 p = __builtin_nontemporal_load((const u32x4*)pk + c);
+    const uint32_t s = sc[nat];
+    buf[lpos] = dequant8(p.x, s);
+    buf[lpos + 1] = dequant8(p.y, s);
+    buf[lpos + 2] = dequant8(p.z, s);
+    buf[lpos + 3] = dequant8(p.w, s);
+  }
+  __syncthreads();
+  const int64_t nvalid = nchunks - c0;  // chunks of this workgroup (<= 256 in its last one)
 #pragma unroll
-      for (int j = 1; j < kDequantMaxJobs; ++j)
-        if (j == q) {
-          pk = J.packed[j];
-          sc = J.scales[j];
-          ot = J.out[j];
-          kc = J.kc[j];
-          tl = J.tiled[j];
-          t = c - J.start[j];
-        }
-      int64_t nat = t;  // checkpoint-layout chunk index n * K/32 + cb
-      if (tl) {
-        const int L = (int)(t & 63);
-        const int64_t qq = t >> 6;
-        const int ji = (int)(qq & 1);
-        const int64_t nst = kc >> 3;
-        const int64_t j = (qq >> 1) % nst, nt = (qq >> 1) / nst;
-        nat = (16 * nt + (L & 15)) * kc + 8 * j + 2 * (L >> 4) + ji;
-      }
-      p[i] = __builtin_nontemporal_load((const u32x4*)pk + t);
-      s[i] = sc[nat];
-      o[i] = (u32x4*)ot + 4 * nat;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int slot = pass * 256 + t;  // 16-byte output piece of buf
+    if (tl) {
+      // unit (pass / 2) of the workgroup: rows 8 (pass % 2) + t / 32, bytes 16 (t % 32) of a 512-byte segment
+      const int unit = pass >> 1;
+      if (128 * unit >= nvalid) continue;
+      const int64_t u = (c0 >> 7) + unit;
+      const int r = 8 * (pass & 1) + (t >> 5);
+      const int64_t n = 16 * (u / nst) + r;
+      __builtin_nontemporal_store(buf[slot], (u32x4*)ot + n * (kc * 4) + 32 * (u % nst) + (t & 31));
+    } else {
+      if (slot / 4 >= nvalid) continue;
+      __builtin_nontemporal_store(buf[slot], (u32x4*)ot + c0 * 4 + slot);
     }
   }
-#pragma unroll
-  for (int i = 0; i < kDequantChunksPerThread; ++i)
-    if (o[i]) {
-      __builtin_nontemporal_store(dequant8(p[i].x, s[i]), o[i]);
-      __builtin_nontemporal_store(dequant8(p[i].y, s[i]), o[i] + 1);
-      __builtin_nontemporal_store(dequant8(p[i].z, s[i]), o[i] + 2);
-      __builtin_nontemporal_store(dequant8(p[i].w, s[i]), o[i] + 3);
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -335,12 +342,15 @@ hipError_t launch_mxfp4_dequant(const uint8_t* packed, const uint8_t* scales, ui
 
 hipError_t launch_mxfp4_dequant_multi(const Dsv4DequantJobs& jobs, hipStream_t st) {
   if (jobs.n < 1 || jobs.n > kDequantMaxJobs) return hipErrorInvalidValue;
-  const int64_t n_chunks = jobs.start[jobs.n];
-  if (n_chunks == 0) return hipSuccess;
-  const int64_t per_wg = 256LL * kDequantChunksPerThread;
-  const int64_t grid = (n_chunks + per_wg - 1) / per_wg;
+  Dsv4DequantJobs J = jobs;
+  int64_t grid = 0;
+  for (int q = 0; q < J.n; ++q) {  // whole workgroups of 256 chunks per tensor
+    J.wg_start[q] = grid;
+    grid += (J.start[q + 1] - J.start[q] + 255) / 256;
+  }
+  if (grid == 0) return hipSuccess;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(mxfp4_dequant_multi_kernel, dim3((unsigned)grid), dim3(256), 0, st, jobs);
+  hipLaunchKernelGGL(mxfp4_dequant_multi_kernel, dim3((unsigned)grid), dim3(256), 0, st, J);
   return hipGetLastError();
 }
 
