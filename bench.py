@@ -760,7 +760,8 @@ def main():
         if args.only in ("", "prefill", "compute"):
             # the compute-bound point: 16384 tokens x top-8 = 131072 routed rows, every expert
             # with hundreds of rows, arithmetic intensity ~1.9 kFLOP/B (MXFP4 ridge ~1.26 kFLOP/B)
-            legs += [("bf16_prefill_16384", 16384, PROFILE_BF16), ("a4w4_prefill_16384", 16384, PROFILE_A4W4)]
+            legs += [("bf16_prefill_16384", 16384, PROFILE_BF16), ("a4w4_prefill_16384", 16384, PROFILE_A4W4),
+                     ("bf16_pure_prefill_16384", 16384, PROFILE_BF16_PURE)]
         for name, Tn, prof in legs:
             host = routing_batches(2 if Tn > 2048 else 4, Tn, K, 21 + Tn)
             dev_b = [(x.to(dev), torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(dev))

@@ -340,8 +340,9 @@ static int check_gemm_common(int afmt, const void* a, const void* a_scale, const
                              const void* experts, int Kdim, void* out) {
   REQUIRE(afmt == DSV4_AFMT_E4M3 || afmt == DSV4_AFMT_E2M1 || afmt == DSV4_AFMT_BF16, DSV4_ERR_UNSUPPORTED,
           "gemm: unknown A format %d", afmt);
-  REQUIRE(afmt != DSV4_AFMT_BF16 || block_m == DSV4_GEMM_BLOCK_M || block_m == 64, DSV4_ERR_UNSUPPORTED,
-          "gemm: bf16 activations need block_m %d or 64 (got %d)", DSV4_GEMM_BLOCK_M, block_m);
+  REQUIRE(afmt != DSV4_AFMT_BF16 || block_m == DSV4_GEMM_BLOCK_M || block_m == 64 || block_m == 256,
+          DSV4_ERR_UNSUPPORTED, "gemm: bf16 activations need block_m %d, 64 or 256 (got %d)", DSV4_GEMM_BLOCK_M,
+          block_m);
   REQUIRE(R >= 0 && max_blocks >= 0, DSV4_ERR_SHAPE, "gemm: negative size");
   REQUIRE(moe_gemm_supported_kdim(Kdim), DSV4_ERR_UNSUPPORTED,
           "gemm: reduction dim %d unsupported (512, 1024, 2048 or 4096)", Kdim);
@@ -428,13 +429,18 @@ struct LayerWs {
 //   a4w4 below 32,768 rows, where the large-tile launch takes half blocks as well and
 //   runs beside the tiled one: a 128-row threshold gained 3 % at 2048 tokens (1.011-1.018
 //   -> 0.981-0.984 ms), 256 lost 4 %.
+//   pure bf16 (bf16 large-tile kernel, whole blocks, 128-row threshold): layer ms with
+//   / without the split at 2048 tokens 1.682-1.689 / 1.570, 4096 2.588-2.604 / 2.451,
+//   8192 4.087-4.096 / 4.106-4.112, 16384 7.20-7.33 / 7.41; bf16 MFMAs take the same
+//   time on either kernel per useful FLOP until the hot experts fill many whole blocks,
+//   so the pure variant splits from 65,536 routed rows.
 // DSV4_HOT_LAYER_ROWS and DSV4_HOT_ROWS (0: never) override them, read once.
-static int64_t hot_layer_rows(bool /*fp8*/) {
+static int64_t hot_layer_rows(bool pure) {
   static const int64_t v = [] {
     const char* s = getenv("DSV4_HOT_LAYER_ROWS");
     return s ? (int64_t)atoll(s) : (int64_t)-1;
   }();
-  return v >= 0 ? v : 16384;
+  return v >= 0 ? v : pure ? 65536 : 16384;
 }
 
 static int hot_rows_threshold(int64_t R, bool fp8) {
@@ -477,8 +483,8 @@ static LayerWs layer_ws(int T, int K, int E, int D, int I, int profile, bool sha
   w.out = take(2 * Rt * D);
   w.align_scratch = R > kAlignSmallRows ? take(align_chunked_scratch_bytes((int)R, E)) : 0;
   w.route_part = routed ? take(dsv4_moe_route_workspace_bytes(T, D, E)) : -1;  // router partial logits
-  const int hot = hot_rows_threshold(R, fp8);
-  if (!pure && R >= hot_layer_rows(fp8) && R > kAlignSmallRows && hot > 0 && moe_gemm_big_supported(D, I, true) &&
+  const int hot = hot_rows_threshold(R, fp8 || pure);
+  if (R >= hot_layer_rows(pure) && R > kAlignSmallRows && hot > 0 && moe_gemm_big_supported(D, I, true) &&
       moe_gemm_big_supported(I, D, false)) {
     w.hot_min = hot;
     // each hot expert holds >= hot_min rows: blocks <= R/256 + min(E, R/hot_min) + 1
@@ -705,14 +711,16 @@ static int layer_forward(int profile, int scale_rule, const void* x, const void*
   // Under stream capture the layer keeps one stream: the shared side stream would
   // join the caller's capture, and another thread's layer on this device could then
   // put its work into that graph.
-  if (!one_stream && w.hot_min > 0 && hq_fused && hot_concurrent()) {
+  // (the pure-bf16 variant has no h quantisation launch between the GEMMs either)
+  const bool hot_side = w.hot_min > 0 && (hq_fused || pure);
+  if (!one_stream && hot_side && hot_concurrent()) {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing((hipStream_t)stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
       one_stream = true;
   }
   SideStream* side = nullptr;
   std::unique_lock<std::mutex> side_lock;
-  if (w.hot_min > 0 && hq_fused && !one_stream && hot_concurrent()) {
+  if (hot_side && !one_stream && hot_concurrent()) {
     rc = side_stream(stream, &side);
     if (rc) return rc;
     side_lock = std::unique_lock<std::mutex>(side->mu);

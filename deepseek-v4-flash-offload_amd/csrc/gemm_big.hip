@@ -321,6 +321,126 @@ DSV4_DEV void big_tile_of_block(int& mb, int& nt) {
   nt = 8 * (gi % ngroups) + (w & 7);
 }
 
+// Epilogue of a large-tile workgroup (every wave is past the operand ring, so the LDS is
+// free): gate/up - SwiGLU x routing weight, bf16 h and/or its quantisation (hq_mode);
+// down - bf16 outputs. acc[tt][wt]: register r of lane l = weight column 8(r/4) + 4(l/32) +
+// r%4 of the wave's weight tile wt, token l%32 of its token tile tt. G: the workgroup shape
+// (BM rows, WM x WN waves of TT x WT tiles).
+template <class G, bool GATEUP>
+DSV4_DEV void big_epilogue(const Dsv4GemmArgs& p, v16f (&acc)[G::TT][G::WT], uint8_t* lds, int c0, int wm, int wn,
+                           int r32, int g2, const int* fr, const float* wr) {
+  constexpr int kBM = G::BM, H = G::WT / 2;
+  if (GATEUP) {
+    const int cw = c0 + 32 * H * wn;  // this wave's first of 32 H intermediate columns
+    // h for columns cw + 32 h + 8 q + 4 g2 + e of token tile tt, packed bf16 pairs
+    uint32_t hp[G::TT][H][4][2];
+    float rmax[G::TT][H];  // per 32-column block, this lane's half of it
+#pragma unroll
+    for (int tt = 0; tt < G::TT; ++tt)
+#pragma unroll
+      for (int h = 0; h < H; ++h) {
+        float m = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; e += 2) {
+            const int r = 4 * q + e;
+            // gate (tile h) and up (tile H + h) of the same column, rounded to bf16
+            const uint32_t gu0 = pk_bf16(acc[tt][h][r], acc[tt][H + h][r]);
+            const uint32_t gu1 = pk_bf16(acc[tt][h][r + 1], acc[tt][H + h][r + 1]);
+            const uint32_t hw = pk_bf16(big_swiglu(bf16_lo(gu0), bf16_hi(gu0), wr[tt], p.swiglu_limit),
+                                        big_swiglu(bf16_lo(gu1), bf16_hi(gu1), wr[tt], p.swiglu_limit));
+            hp[tt][h][q][e >> 1] = hw;
+            m = fmaxf(m, fmaxf(fabsf(bf16_lo(hw)), fabsf(bf16_hi(hw))));
+          }
+        rmax[tt][h] = m;
+      }
+    if (!p.hq_skip_h && p.out) {
+#pragma unroll
+      for (int tt = 0; tt < G::TT; ++tt)
+        if (fr[tt] < p.R)
+#pragma unroll
+          for (int h = 0; h < H; ++h)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+              *(v2u*)(p.out + (int64_t)fr[tt] * p.N + cw + 32 * h + 8 * q + 4 * g2) =
+                  v2u{hp[tt][h][q][0], hp[tt][h][q][1]};
+            }
+    }
+    if (p.hq_mode == 2) {  // MXFP4 h: one 32-column block per (tt, h), half of it in each lane of a pair
+#pragma unroll
+      for (int tt = 0; tt < G::TT; ++tt)
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+          const int k = dsv4::mxfp4_block_exp(max_pair(rmax[tt][h]), p.hq_rule);
+          const float inv = dsv4::pow2f(-k);
+          if (fr[tt] < p.R) {
+            const int col = cw + 32 * h;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t w0 = hp[tt][h][q][0], w1 = hp[tt][h][q][1];
+              const uint32_t nib = pk_fp4x2(bf16_lo(w0), bf16_hi(w0), inv, p.hq_rule) |
+                                   pk_fp4x2(bf16_lo(w1), bf16_hi(w1), inv, p.hq_rule) << 8;
+              *(uint16_t*)(p.hq_codes + (int64_t)fr[tt] * (p.N / 2) + (col + 8 * q + 4 * g2) / 2) = (uint16_t)nib;
+            }
+            if (g2 == 0) p.hq_scale[(int64_t)fr[tt] * (p.N / 32) + col / 32] = (uint8_t)(k + 127);
+          }
+        }
+    } else if (p.hq_mode == 1) {  // FP8 h: one 128-column block per token, split over the WN waves of a row
+      float* am = (float*)lds;     // [WN][kBM rows]
+      float bm[G::TT];
+#pragma unroll
+      for (int tt = 0; tt < G::TT; ++tt) {
+        float m = rmax[tt][0];
+#pragma unroll
+        for (int h = 1; h < H; ++h) m = fmaxf(m, rmax[tt][h]);
+        if (g2 == 0) am[wn * kBM + (kBM / G::WM) * wm + 32 * tt + r32] = max_pair(m);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int tt = 0; tt < G::TT; ++tt) {
+        const int row = (kBM / G::WM) * wm + 32 * tt + r32;
+        bm[tt] = am[row];
+#pragma unroll
+        for (int w = 1; w < G::WN; ++w) bm[tt] = fmaxf(bm[tt], am[w * kBM + row]);
+      }
+#pragma unroll
+      for (int tt = 0; tt < G::TT; ++tt) {
+        const int k = dsv4::fp8_block_exp(bm[tt]);
+        const float inv = dsv4::pow2f(-k);
+        if (fr[tt] < p.R) {
+#pragma unroll
+          for (int h = 0; h < H; ++h)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t w0 = hp[tt][h][q][0], w1 = hp[tt][h][q][1];
+              *(uint32_t*)(p.hq_codes + (int64_t)fr[tt] * p.N + cw + 32 * h + 8 * q + 4 * g2) =
+                  pk_fp8x4(bf16_lo(w0), bf16_hi(w0), bf16_lo(w1), bf16_hi(w1), inv);
+            }
+          if (g2 == 0)
+#pragma unroll
+            for (int h = 0; h < H; ++h) p.hq_scale[(int64_t)fr[tt] * (p.N / 32) + cw / 32 + h] = (uint8_t)(k + 127);
+        }
+      }
+    }
+  } else {
+    const int cw = c0 + 32 * G::WT * wn;  // this wave's first output column
+#pragma unroll
+    for (int tt = 0; tt < G::TT; ++tt)
+      if (fr[tt] < p.R)
+#pragma unroll
+        for (int wt = 0; wt < G::WT; ++wt)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+            const int r = 4 * q;
+            *(v2u*)(p.out + (int64_t)fr[tt] * p.N + cw + 32 * wt + 8 * q + 4 * g2) =
+                v2u{pk_bf16(acc[tt][wt][r], acc[tt][wt][r + 1]), pk_bf16(acc[tt][wt][r + 2], acc[tt][wt][r + 3])};
+          }
+  }
+}
+
 template <int AFMT, bool HALF, bool GATEUP>
 __global__ __launch_bounds__((Cfg<AFMT, HALF>::NT), (Cfg<AFMT, HALF>::WGS)) void moe_gemm_big_kernel(Dsv4GemmArgs p) {
   using C = Big<AFMT, HALF>;
@@ -469,116 +589,211 @@ __global__ __launch_bounds__((Cfg<AFMT, HALF>::NT), (Cfg<AFMT, HALF>::WGS)) void
   }
   wait_loads_barrier<0>();  // every wave is done with the ring
 
-  // epilogue (every wave is past the ring: the LDS is free)
-  if (GATEUP) {
-    const int cw = c0 + 32 * H * wn;  // this wave's first of 32 H intermediate columns
-    // h for columns cw + 32 h + 8 q + 4 g2 + e of token tile tt, packed bf16 pairs
-    uint32_t hp[G::TT][H][4][2];
-    float rmax[G::TT][H];  // per 32-column block, this lane's half of it
+  big_epilogue<G, GATEUP>(p, acc, lds, c0, wm, wn, r32, g2, fr, wr);
+}
+
+
+// ---- bf16 activations: the pure-bf16 variant ----------------------------------------
+// Whole 256-row blocks x 256 weight rows, one workgroup of eight waves per CU (4 token
+// groups x 2 weight groups: a wave owns 64 tokens x 128 weight rows = 2 x 4 tiles of
+// 32 x 32), two waves per SIMD. Tokens (bf16, 128 bytes per row per 64-k stage) and the
+// E2M1 weights (chunks as in the kernel above) move by LDS-DMA into a ring of three
+// stages, the weight rows' E8M0 bytes per 1024-k super-stage. A stage's 64 k run as four
+// 16-k chunks: in chunk c, lane (r, g) of weight tile wt turns the 4 bytes of its stage
+// fragment at k 32 g + 8 c .. +8 into 8 bf16 with the hardware scaled converter (exact:
+// an E2M1 value times 2^(s-127) is a bf16 value), takes the 8 bf16 of its token at the
+// same k, and v_mfma_f32_32x32x16_bf16 sums the 16 k the two lane halves hold: both
+// operands carry the same k in the same lane positions, so the instruction's own k order
+// does not matter. Products are exact in fp32, sums fp32. A stage's fragments are read
+// during the stage, after its barrier (two stages of loads stay in flight), the next
+// chunk's tokens ahead of the current chunk's MFMAs.
+//   token chunk c (1 KB): tokens 8c + r (r < 8); slot 8r + (p ^ r) holds bytes
+//                         [16p, 16p + 16) of token r's stage (the 16 lanes of a read
+//                         pass land on distinct bank groups, two tokens per group).
+struct CfgBf {
+  static constexpr int BM = 256, NT = 512, NW = 8, WM = 4, WN = 2, TT = 2, WT = 4;
+};
+namespace bfk {
+constexpr int ACH = 32;                 // 1-KB token chunks per stage
+constexpr int BCH = 8;                  // 1-KB weight chunks per stage
+constexpr int STAGE = (ACH + BCH) * 1024;
+constexpr int NB = 3;                   // ring slots
+constexpr int SCL = 2 * kBN * 16;       // weight scales of one super-stage: [half][row] x 16 bytes
+constexpr int AS_OFF = NB * STAGE;
+constexpr int LDS = AS_OFF + 2 * SCL;
+constexpr int AV = ACH / CfgBf::NW, BV = BCH / CfgBf::NW, L = AV + BV;  // loads per thread per stage
+constexpr int SV = SCL / (CfgBf::NT * 16);                               // per super-stage
+static_assert(LDS <= 160 * 1024, "ring and scale buffers fit the LDS");
+static_assert(AV * CfgBf::NW == ACH && BV * CfgBf::NW == BCH && SV * CfgBf::NT * 16 == SCL, "loads per thread");
+static_assert(L * (NB - 1) + SV < 64, "vmcnt holds 6 bits");
+}  // namespace bfk
+
+typedef __bf16 bfx8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bfx2 __attribute__((ext_vector_type(2)));
+
+// 2^(b - 127) for an E8M0 byte b, branch-free: the byte is the fp32 exponent field
+// (255 gives +inf, as the reference's pow does), except 0, the subnormal 2^-127
+DSV4_DEV float e8m0_scale(uint32_t b) { return __uint_as_float(b ? b << 23 : 0x00400000u); }
+
+// 8 bf16 of the 4 packed bytes w (low nibble first) times `scale` (exact)
+DSV4_DEV bfx8 dequant8_bf16(uint32_t w, float scale) {
+  const bfx2 a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0);
+  const bfx2 b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1);
+  const bfx2 c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2);
+  const bfx2 d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3);
+  return bfx8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+template <bool GATEUP>
+__global__ __launch_bounds__(512, 1) void moe_gemm_big_bf16_kernel(Dsv4GemmArgs p) {
+  using G = CfgBf;
+  constexpr int kBM = G::BM;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[bfk::LDS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / G::WN, wn = wave % G::WN;
+  int mb, nt;
+  big_tile_of_block(mb, nt);
+  if (mb * kHB >= p.num_post_padded[0]) return;  // also every block of the grid's padding
+  const int e = p.block_expert[mb];
+  const Dsv4ExpertPtrs ex = p.experts[e];
+  const bool have_w = GATEUP ? (ex.w1p && ex.w1s && ex.w3p && ex.w3s) : (ex.w2p && ex.w2s);
+  const int NST = p.Kdim / kKS;
+  const int wrow_bytes = p.Kdim / 2, srow = p.Kdim / 32;
+  const int c0 = nt * (GATEUP ? 128 : 256);  // first intermediate column / output row of W2
+  const int slot0 = mb * kHB;
+
+  // this lane's token piece per token load (stage 0): chunk wave * AV + v, token 8c + lane / 8
+  const uint8_t* a_src[bfk::AV];
 #pragma unroll
-    for (int tt = 0; tt < G::TT; ++tt)
-#pragma unroll
-      for (int h = 0; h < H; ++h) {
-        float m = 0.0f;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-          for (int e = 0; e < 4; e += 2) {
-            const int r = 4 * q + e;
-            // gate (tile h) and up (tile H + h) of the same column, rounded to bf16
-            const uint32_t gu0 = pk_bf16(acc[tt][h][r], acc[tt][H + h][r]);
-            const uint32_t gu1 = pk_bf16(acc[tt][h][r + 1], acc[tt][H + h][r + 1]);
-            const uint32_t hw = pk_bf16(big_swiglu(bf16_lo(gu0), bf16_hi(gu0), wr[tt], p.swiglu_limit),
-                                        big_swiglu(bf16_lo(gu1), bf16_hi(gu1), wr[tt], p.swiglu_limit));
-            hp[tt][h][q][e >> 1] = hw;
-            m = fmaxf(m, fmaxf(fabsf(bf16_lo(hw)), fabsf(bf16_hi(hw))));
-          }
-        rmax[tt][h] = m;
-      }
-    if (!p.hq_skip_h && p.out) {
-#pragma unroll
-      for (int tt = 0; tt < G::TT; ++tt)
-        if (fr[tt] < p.R)
-#pragma unroll
-          for (int h = 0; h < H; ++h)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              typedef uint32_t v2u __attribute__((ext_vector_type(2)));
-              *(v2u*)(p.out + (int64_t)fr[tt] * p.N + cw + 32 * h + 8 * q + 4 * g2) =
-                  v2u{hp[tt][h][q][0], hp[tt][h][q][1]};
-            }
-    }
-    if (p.hq_mode == 2) {  // MXFP4 h: one 32-column block per (tt, h), half of it in each lane of a pair
-#pragma unroll
-      for (int tt = 0; tt < G::TT; ++tt)
-#pragma unroll
-        for (int h = 0; h < H; ++h) {
-          const int k = dsv4::mxfp4_block_exp(max_pair(rmax[tt][h]), p.hq_rule);
-          const float inv = dsv4::pow2f(-k);
-          if (fr[tt] < p.R) {
-            const int col = cw + 32 * h;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const uint32_t w0 = hp[tt][h][q][0], w1 = hp[tt][h][q][1];
-              const uint32_t nib = pk_fp4x2(bf16_lo(w0), bf16_hi(w0), inv, p.hq_rule) |
-                                   pk_fp4x2(bf16_lo(w1), bf16_hi(w1), inv, p.hq_rule) << 8;
-              *(uint16_t*)(p.hq_codes + (int64_t)fr[tt] * (p.N / 2) + (col + 8 * q + 4 * g2) / 2) = (uint16_t)nib;
-            }
-            if (g2 == 0) p.hq_scale[(int64_t)fr[tt] * (p.N / 32) + col / 32] = (uint8_t)(k + 127);
-          }
-        }
-    } else if (p.hq_mode == 1) {  // FP8 h: one 128-column block per token, split over the WN waves of a row
-      float* am = (float*)lds;     // [WN][kBM rows]
-      float bm[G::TT];
-#pragma unroll
-      for (int tt = 0; tt < G::TT; ++tt) {
-        float m = rmax[tt][0];
-#pragma unroll
-        for (int h = 1; h < H; ++h) m = fmaxf(m, rmax[tt][h]);
-        if (g2 == 0) am[wn * kBM + (kBM / G::WM) * wm + 32 * tt + r32] = max_pair(m);
-      }
-      __syncthreads();
-#pragma unroll
-      for (int tt = 0; tt < G::TT; ++tt) {
-        const int row = (kBM / G::WM) * wm + 32 * tt + r32;
-        bm[tt] = am[row];
-#pragma unroll
-        for (int w = 1; w < G::WN; ++w) bm[tt] = fmaxf(bm[tt], am[w * kBM + row]);
-      }
-#pragma unroll
-      for (int tt = 0; tt < G::TT; ++tt) {
-        const int k = dsv4::fp8_block_exp(bm[tt]);
-        const float inv = dsv4::pow2f(-k);
-        if (fr[tt] < p.R) {
-#pragma unroll
-          for (int h = 0; h < H; ++h)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const uint32_t w0 = hp[tt][h][q][0], w1 = hp[tt][h][q][1];
-              *(uint32_t*)(p.hq_codes + (int64_t)fr[tt] * p.N + cw + 32 * h + 8 * q + 4 * g2) =
-                  pk_fp8x4(bf16_lo(w0), bf16_hi(w0), bf16_lo(w1), bf16_hi(w1), inv);
-            }
-          if (g2 == 0)
-#pragma unroll
-            for (int h = 0; h < H; ++h) p.hq_scale[(int64_t)fr[tt] * (p.N / 32) + cw / 32 + h] = (uint8_t)(k + 127);
-        }
-      }
-    }
-  } else {
-    const int cw = c0 + 32 * G::WT * wn;  // this wave's first output column
-#pragma unroll
-    for (int tt = 0; tt < G::TT; ++tt)
-      if (fr[tt] < p.R)
-#pragma unroll
-        for (int wt = 0; wt < G::WT; ++wt)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            typedef uint32_t v2u __attribute__((ext_vector_type(2)));
-            const int r = 4 * q;
-            *(v2u*)(p.out + (int64_t)fr[tt] * p.N + cw + 32 * wt + 8 * q + 4 * g2) =
-                v2u{pk_bf16(acc[tt][wt][r], acc[tt][wt][r + 1]), pk_bf16(acc[tt][wt][r + 2], acc[tt][wt][r + 3])};
-          }
+  for (int v = 0; v < bfk::AV; ++v) {
+    const int c = wave * bfk::AV + v, r = lane >> 3;
+    const int f = p.sorted_ids[slot0 + 8 * c + r];
+    const int arow = f < p.R ? f / p.a_row_div : 0;  // padding rows read row 0 (never stored)
+    a_src[v] = p.a + (int64_t)arow * p.a_row_bytes + 16 * ((lane & 7) ^ r);
   }
+  // weight pieces as in moe_gemm_big_kernel
+  const bool tiled = tiled_ptr(GATEUP ? ex.w1p : ex.w2p);
+  const int bj = tiled ? 2048 : 4 * (kKS / 2), bg = tiled ? 256 : kKS / 2;
+  const uint8_t* b_src[bfk::BV];
+#pragma unroll
+  for (int v = 0; v < bfk::BV; ++v) {
+    const int q = (wave * bfk::BV + v) * 64 + lane;
+    const int tile = q >> 5, ji = (q >> 4) & 1, r = q & 15;
+    const int gtile = c0 / 16 + (GATEUP ? (tile & 7) : tile);
+    const uint8_t* w = untag(GATEUP ? (tile < 8 ? ex.w1p : ex.w3p) : ex.w2p);
+    b_src[v] = w + (tiled ? (int64_t)((gtile * (p.Kdim / 256)) * 2 + ji) * 1024 + 16 * r
+                          : (int64_t)(16 * gtile + r) * wrow_bytes + 16 * ji);
+  }
+  // this lane's weight-scale piece per super-stage: half q / kBN, row q % kBN of a buffer
+  const uint8_t* sc_src[bfk::SV];
+#pragma unroll
+  for (int v = 0; v < bfk::SV; ++v) {
+    const int q = (wave * bfk::SV + v) * 64 + lane;
+    const int half = q / kBN, row = q % kBN;
+    const uint8_t* ws = GATEUP ? (row < 128 ? ex.w1s : ex.w3s) : ex.w2s;
+    sc_src[v] = ws + (int64_t)(GATEUP ? c0 + (row & 127) : c0 + row) * srow + 16 * half;
+  }
+
+  v16f acc[G::TT][G::WT];
+#pragma unroll
+  for (int tt = 0; tt < G::TT; ++tt)
+#pragma unroll
+    for (int wt = 0; wt < G::WT; ++wt) acc[tt][wt] = v16f{};
+  const int r32 = lane & 31, g2 = lane >> 5;
+  int fr[G::TT];
+  float wr[G::TT];
+#pragma unroll
+  for (int tt = 0; tt < G::TT; ++tt) {
+    fr[tt] = p.sorted_ids[slot0 + (kBM / G::WM) * wm + 32 * tt + r32];
+    wr[tt] = GATEUP && fr[tt] < p.R ? p.topk_w[fr[tt]] : 0.0f;
+  }
+  constexpr int H = G::WT / 2;
+  int brow0[G::WT];
+#pragma unroll
+  for (int wt = 0; wt < G::WT; ++wt)
+    brow0[wt] = GATEUP ? (wt / H) * 128 + 32 * (H * wn + wt % H) : 32 * (G::WT * wn + wt);
+  const int b_lane = 16 * (32 * (r32 >> 4) + 16 * g2 + (r32 & 15));
+  // this lane's token in each tile: its chunk and row in the chunk (tiles start on chunk edges)
+  int tchunk[G::TT];
+#pragma unroll
+  for (int tt = 0; tt < G::TT; ++tt) tchunk[tt] = ((kBM / G::WM) * wm + 32 * tt + r32) >> 3;
+  const int tr = r32 & 7;
+
+  if (have_w) {  // uniform per workgroup: every wave reaches every barrier
+    // Stage s lives in ring slot s % NB. At the top of stage s this wave waits until its
+    // own loads of stage s have landed (those of stage s + 1 may still fly), then the
+    // barrier: every wave's share of stage s is in the LDS and every wave is done reading
+    // stage s - 1, whose slot takes the loads of stage s + NB - 1. Past the last stage the
+    // loads repeat stage NST - 1 into slots never read again (no branch in the loop).
+    // Scales: super-stage ss in buffer ss % 2, loaded after the barrier of stage 16 ss
+    // (stage 16 ss - 1, the last reader of that buffer's previous super-stage, is done).
+    const int NSS = NST / kSS;
+#pragma unroll
+    for (int v = 0; v < bfk::SV; ++v) dma16(sc_src[v], lds + bfk::AS_OFF + (wave * bfk::SV + v) * 1024);
+#pragma unroll
+    for (int t = 0; t < bfk::NB - 1; ++t) {
+#pragma unroll
+      for (int v = 0; v < bfk::AV; ++v) dma16(a_src[v] + t * 128, lds + t * bfk::STAGE + (wave * bfk::AV + v) * 1024);
+      const int boff = (t >> 2) * bj + (t & 3) * bg;
+#pragma unroll
+      for (int v = 0; v < bfk::BV; ++v)
+        dma16(b_src[v] + boff, lds + t * bfk::STAGE + (bfk::ACH + wave * bfk::BV + v) * 1024);
+    }
+    int slot = 0, fill = bfk::NB - 1;
+    auto step = [&](int s) {
+      wait_loads_barrier<bfk::L * (bfk::NB - 2)>();
+      const int sl = min(s + bfk::NB - 1, NST - 1);
+      uint8_t* fs = lds + fill * bfk::STAGE;
+#pragma unroll
+      for (int v = 0; v < bfk::AV; ++v) dma16(a_src[v] + sl * 128, fs + (wave * bfk::AV + v) * 1024);
+      const int boff = (sl >> 2) * bj + (sl & 3) * bg;
+#pragma unroll
+      for (int v = 0; v < bfk::BV; ++v) dma16(b_src[v] + boff, fs + (bfk::ACH + wave * bfk::BV + v) * 1024);
+      const uint8_t* Ls = lds + slot * bfk::STAGE;
+      const uint8_t* S = lds + bfk::AS_OFF + ((s / kSS) & 1) * bfk::SCL;
+      const int q = 2 * (s % kSS) + g2;  // this lane's 32-k block of the super-stage
+      v4i wf[G::WT];
+      float wsc[G::WT];
+#pragma unroll
+      for (int wt = 0; wt < G::WT; ++wt) {
+        wf[wt] = *(const v4i*)(Ls + (bfk::ACH + brow0[wt] / 32) * 1024 + b_lane);
+        wsc[wt] = e8m0_scale(S[((q >> 4) * kBN + brow0[wt] + r32) * 16 + (q & 15)]);
+      }
+      bfx8 tk[2][G::TT];
+#pragma unroll
+      for (int tt = 0; tt < G::TT; ++tt)
+        tk[0][tt] = *(const bfx8*)(Ls + tchunk[tt] * 1024 + 16 * (8 * tr + ((4 * g2) ^ tr)));
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (c < 3) {
+#pragma unroll
+          for (int tt = 0; tt < G::TT; ++tt)
+            tk[(c + 1) & 1][tt] = *(const bfx8*)(Ls + tchunk[tt] * 1024 + 16 * (8 * tr + ((4 * g2 + c + 1) ^ tr)));
+        }
+        bfx8 wb[G::WT];
+#pragma unroll
+        for (int wt = 0; wt < G::WT; ++wt) wb[wt] = dequant8_bf16((uint32_t)wf[wt][c], wsc[wt]);
+#pragma unroll
+        for (int tt = 0; tt < G::TT; ++tt)
+#pragma unroll
+          for (int wt = 0; wt < G::WT; ++wt)
+            acc[tt][wt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wb[wt], tk[c & 1][tt], acc[tt][wt], 0, 0, 0);
+      }
+      slot = slot + 1 == bfk::NB ? 0 : slot + 1;
+      fill = fill + 1 == bfk::NB ? 0 : fill + 1;
+    };
+#pragma unroll 1
+    for (int ss = 0; ss < NSS; ++ss) {
+      step(kSS * ss);
+#pragma unroll
+      for (int v = 0; v < bfk::SV; ++v)
+        dma16(sc_src[v] + min(ss + 1, NSS - 1) * 32, lds + bfk::AS_OFF + ((ss + 1) & 1) * bfk::SCL + (wave * bfk::SV + v) * 1024);
+#pragma unroll 1
+      for (int s = kSS * ss + 1; s < kSS * (ss + 1); ++s) step(s);
+    }
+  }
+  wait_loads_barrier<0>();  // every wave is done with the ring
+  big_epilogue<G, GATEUP>(p, acc, lds, c0, wm, wn, r32, g2, fr, wr);
 }
 
 }  // namespace
@@ -603,6 +818,13 @@ hipError_t launch_moe_gemm_big(const Dsv4GemmArgs& a, bool gateup, hipStream_t s
   if (a.block_m != kHB || !moe_gemm_big_supported(a.Kdim, a.N, gateup)) return hipErrorInvalidValue;
   if (a.max_blocks <= 0) return hipSuccess;
   const int ntiles = a.N / (gateup ? 128 : 256);
+  if (a.afmt == kAfmtBf16) {  // pure bf16: whole blocks, bf16 MFMA on in-register dequantised weights
+    if (gateup && a.hq_mode) return hipErrorInvalidValue;
+    const dim3 grid(ntiles, ntiles % 8 == 0 ? (a.max_blocks + 31) / 32 * 32 : a.max_blocks);
+    if (gateup) hipLaunchKernelGGL((moe_gemm_big_bf16_kernel<true>), grid, dim3(CfgBf::NT), 0, st, a);
+    else hipLaunchKernelGGL((moe_gemm_big_bf16_kernel<false>), grid, dim3(CfgBf::NT), 0, st, a);
+    return hipGetLastError();
+  }
   // workgroup shape (Cfg): half blocks for E4M3, and for E2M1 while the layer's rows
   // are too few to fill the CUs with whole blocks
   if (a.afmt == 0) launch_big<0, true>(a, gateup, ntiles, st);

@@ -35,7 +35,8 @@ extern "C" {
 #define DSV4_AFMT_E4M3 0 /* one E4M3fn code per byte, E8M0 per 32 (bf16 profile) */
 #define DSV4_AFMT_E2M1 1 /* two E2M1 codes per byte, E8M0 per 32 (a4w4 profile) */
 #define DSV4_AFMT_BF16 2 /* bf16 rows as they are (a_scale unused), times the exactly dequantised \
-                            bf16 weights on the bf16 MFMA: the pure-bf16 variant; block_m 16 or 64 */
+                            bf16 weights on the bf16 MFMA: the pure-bf16 variant; block_m 16, 64 \
+                            or 256 */
 
 /* profiles of the routed layer */
 #define DSV4_PROFILE_BF16 0 /* deepseek_v4.py:166-197 (FP8 round-trip activations) */
@@ -212,10 +213,10 @@ int dsv4_moe_combine(const void* out_flat, const void* topk_ids, int ids_int64, 
  * [rows, D/2] (E2M1), a_scale [rows, D/32]. h_out: bf16 [R, I] by flat index.
  * block_m (the moe_align block size) is 16 (single-wave workgroups, decode),
  * 64 or 128 (LDS-tiled workgroups: each weight fragment serves 4 or 8 row
- * tiles) or 256 (large-tile workgroups, 32x32x64 MFMAs, E4M3/E2M1 A only: D a
+ * tiles) or 256 (large-tile workgroups: 32x32x64 scaled MFMAs for E4M3/E2M1
+ * A, 32x32x16 bf16 MFMAs on weights dequantised in registers for bf16 A; D a
  * multiple of 1024 for gate/up, I of 1024 and D of 256 for down); D and I must
- * be 256 * 2^n (512..4096) and I a multiple of 128. The bf16 A format takes
- * block_m 16 or 64. */
+ * be 256 * 2^n (512..4096) and I a multiple of 128. */
 int dsv4_moe_gemm_gateup(int afmt, const void* a, const void* a_scale, int a_row_div, const int32_t* sorted_ids,
                          const int32_t* block_expert, const int32_t* num_post_padded, int R, int block_m,
                          int max_blocks, const void* expert_table, int D, int I, const float* topk_w,

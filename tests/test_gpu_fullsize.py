@@ -11,8 +11,10 @@ hidden 4096, inter 2048, at
   rows (the Zipf-hot ones, up to ~14,000 rows) run in 256-row blocks on the
   large-tile kernel, the others in 64-row blocks;
 * 64 tokens in the a4w4 profile: 512 routed rows on the 16-row kernel;
-* 2048 tokens in the pure-bf16 variant (no FP8 round trips): 64-row blocks on
-  the tiled kernel with bf16 activations.
+* 2048 and 16384 tokens in the pure-bf16 variant (no FP8 round trips): bf16
+  activations in 64-row blocks on the tiled kernel; at 16384 tokens (from
+  65,536 routed rows) the hot experts on the large-tile bf16 kernel (32x32x16
+  bf16 MFMAs).
 Expert weights are random bytes generated on the device and stored MFMA-tiled,
 as the slot cache stores them. The oracle reads checkpoint-layout copies of the
 sampled tokens' experts. The sample at 2048 tokens: the tokens of the first and
@@ -58,7 +60,8 @@ def _device_experts(dev, seed):
 
 
 @pytest.mark.parametrize("profile,T", [("bf16", 2048), ("a4w4", 2048), ("a4w4", 64), ("bf16", 4096),
-                                       ("a4w4", 4096), ("bf16", 16384), ("a4w4", 16384), ("bf16_pure", 2048)])
+                                       ("a4w4", 4096), ("bf16", 16384), ("a4w4", 16384), ("bf16_pure", 2048),
+                                       ("bf16_pure", 16384)])
 def test_full_size_layer_on_sampled_tokens(gpu, profile, T):
     ids = synth.zipf_topk(T, K, E, synth.rank_permutation(E, 3), np.random.default_rng(T))
     w = synth.routing_weights(T, K, T + 1)
@@ -102,9 +105,11 @@ def _sample_tokens(ids, T, profile, n_hot=16, n_random=32):
     n_random random tokens; every token when T <= 64. The large-tile split
     (from 16,384 routed rows; only the 8 hottest experts are then taken)
     gives its experts blocks of the rows one workgroup takes: bf16, experts
-    with at least 128 rows, 128 rows (half a hot block); a4w4, experts with
-    at least 128 rows in 128-row halves below 32,768 routed rows, then at
-    least 256 rows (128 from 65,536) in whole 256-row blocks."""
+    with at least 128 rows, 128 rows (half a hot block); pure bf16 (from
+    65,536 routed rows), experts with at least 128 rows in whole 256-row
+    blocks; a4w4, experts with at
+    least 128 rows in 128-row halves below 32,768 routed rows, then at least
+    256 rows (128 from 65,536) in whole 256-row blocks."""
     if T <= 64:
         return np.arange(T)
     R = ids.size
@@ -112,13 +117,14 @@ def _sample_tokens(ids, T, profile, n_hot=16, n_random=32):
     counts = np.bincount(flat, minlength=E)
     picks = set()
     fp8 = profile == "bf16"
-    split = R >= 16384 and profile != "bf16_pure"  # the layer's large-tile split
-    hot_min = 128 if (fp8 or R < 32768 or R >= 65536) else 256
+    pure = profile == "bf16_pure"
+    split = R >= (65536 if pure else 16384)  # the layer's large-tile split
+    hot_min = 128 if (fp8 or pure or R < 32768 or R >= 65536) else 256
     if split:
         n_hot = 8
     for e in np.argsort(-counts, kind="stable")[:n_hot]:
         tok = np.nonzero(flat == e)[0] // ids.shape[1]
-        big = 128 if (fp8 or R < 32768) else 256
+        big = 256 if pure else 128 if (fp8 or R < 32768) else 256
         bm = big if (split and tok.size >= hot_min) else (64 if R >= 2048 else 16)
         for b in range(0, tok.size, bm):
             picks.add(int(tok[b]))

@@ -227,12 +227,16 @@ def test_layer_forward_ceil_rule_and_int32_ids(gpu):
 PURE_ACC_REL = 2.0 ** -16
 
 
-@pytest.mark.parametrize("block_m", [16, 64])
-@pytest.mark.parametrize("T,K,E,D,I", [(24, 4, 16, 1024, 512), (8, 8, 256, 4096, 2048), (200, 8, 16, 512, 512),
-                                       (300, 8, 8, 2048, 1024)])
+_PURE_SHAPES = [(24, 4, 16, 1024, 512), (8, 8, 256, 4096, 2048), (200, 8, 16, 512, 512), (300, 8, 8, 2048, 1024)]
+
+
+@pytest.mark.parametrize("T,K,E,D,I,block_m", [s + (bm,) for bm in (16, 64) for s in _PURE_SHAPES] +
+                         [(8, 8, 256, 4096, 2048, 256), (300, 8, 8, 2048, 1024, 256), (1024, 8, 8, 1024, 1024, 256)])
 def test_grouped_gemm_stages_bf16_pure(gpu, T, K, E, D, I, block_m):
     # 16-row blocks: the single-wave kernel; 64-row blocks: the LDS-tiled kernel
-    # (bf16 A tile in LDS, weight fragments dequantised once per 32-k half)
+    # (bf16 A tile in LDS, weight fragments dequantised once per 32-k half); 256-row
+    # blocks: the large-tile bf16 kernel (32x32x16 bf16 MFMAs, weight fragments
+    # dequantised in registers per 16-k chunk; hidden and inter multiples of 1024)
     from dsv4_hip import AFMT_BF16
     ids, w, xb, host, devw, table = _case(T, K, E, D, I, 71 + T, gpu)
     al = ops.moe_align(_dev(ids, gpu), _dev(w, gpu), E, block_m)
@@ -278,7 +282,7 @@ def test_grouped_gemm_stages_bf16_pure(gpu, T, K, E, D, I, block_m):
                 f"pure bf16 down T={T} block_m={block_m}")
 
 
-@pytest.mark.parametrize("block_m", [16, 64])
+@pytest.mark.parametrize("block_m", [16, 64, 256])
 def test_dequant_in_the_bf16_gemm_every_byte_and_scale(gpu, block_m):
     # one-hot activations pick single weight elements: out[f][n] = W[n][k(f)] exactly, so
     # every packed byte value with every E8M0 byte 0..252 goes through the GEMM's
@@ -286,7 +290,7 @@ def test_dequant_in_the_bf16_gemm_every_byte_and_scale(gpu, block_m):
     # Above 252 some weights are infinite, and 0 x inf would turn whole output columns
     # into NaN, as it does in any dot product with them.
     from dsv4_hip import AFMT_BF16
-    D, I, E = 512, 512, 1
+    D, I, E = (1024, 1024, 1) if block_m == 256 else (512, 512, 1)  # the large-tile kernel: I % 1024 == 0
     rng = np.random.default_rng(5)
     w2p = rng.integers(0, 256, (D, I // 2), dtype=np.uint8)
     w2s = np.tile(np.arange(253, dtype=np.uint8), (D * (I // 32)) // 253 + 1)[:D * (I // 32)].reshape(D, I // 32)
