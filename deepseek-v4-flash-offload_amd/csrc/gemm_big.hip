@@ -109,6 +109,8 @@ struct Big {
   static constexpr int LDS = NB * STAGE + 2 * SCL;
   static_assert(LDS * Cfg<AFMT, HALF>::WGS <= 160 * 1024, "the stage ring and two scale super-stages must fit the LDS");
   static_assert(BCH == 8 && (ACH * 1024) == kBM * (AFMT == 0 ? kKS : kKS / 2), "chunking");
+  static_assert(AV * G::NW == ACH && BV * G::NW == BCH && SV * kNT * 16 == SCL, "loads per thread");
+  static_assert(L * NB + SV < 64, "vmcnt holds 6 bits");
 };
 
 DSV4_DEV bool tiled_ptr(const uint8_t* p) { return ((uintptr_t)p & 1u) != 0; }
@@ -149,14 +151,6 @@ DSV4_DEV void big_dma_scales(uint8_t* lds, int buf, const uint8_t* const* sc_src
   for (int v = 0; v < C::SV; ++v) dma16(sc_src[v] + ss * 32, lds + C::AS_OFF + buf * C::SCL + (wave * C::SV + v) * 1024);
 }
 
-// The E8M0 byte q (0..31, the 32-k block within the super-stage) of row `row` of the
-// A (B = false) or weight (B = true) rows in scale buffer S.
-template <int AFMT, bool HALF, bool B>
-DSV4_DEV int scale_byte(const uint8_t* S, int row, int q) {
-  constexpr int kBM = Cfg<AFMT, HALF>::BM;
-  return S[(B ? kBM * 32 : 0) + ((q >> 4) * (B ? kBN : kBM) + row) * 16 + (q & 15)];
-}
-
 // Issues stage s's loads into ring slot `slot`: this wave's A chunks wave * AV + v and
 // weight chunks wave * BV + v (a_src / b_src: this lane's piece at stage 0; bj / bg:
 // the weight offset per 4 stages / per stage within them, no branch in the loop).
@@ -173,28 +167,23 @@ DSV4_DEV void big_dma_stage(uint8_t* slot, const uint8_t* const* a_src, const ui
   for (int v = 0; v < C::BV; ++v) dma16(b_src[v] + boff, slot + (C::ACH + wave * C::BV + v) * 1024);
 }
 
-// The fragments of one stage for this wave: weight tiles nt (16 bytes + scale each),
-// A tiles mt (E4M3: 2 x 16 bytes, E2M1: 16 bytes; + scale each).
+// The fragments of one stage for this wave: weight tiles nt (16 bytes each), A tiles
+// mt (E4M3: 2 x 16 bytes, E2M1: 16 bytes).
 template <int AFMT, bool HALF>
 struct BigFrag {
   v4i b[Cfg<AFMT, HALF>::WT];
   v4i lo[Cfg<AFMT, HALF>::TT];
   v4i hi[AFMT == 0 ? Cfg<AFMT, HALF>::TT : 1];
-  int sb[Cfg<AFMT, HALF>::WT], sa[Cfg<AFMT, HALF>::TT];
 };
 
-// Reads one stage's fragments from ring slot L. S: the scale super-stage buffer, q0:
-// this stage's first scale byte in it. a_lo / a_hi: this lane's byte offsets inside an
-// A chunk, b_lane inside a weight chunk.
+// Reads one stage's fragments from ring slot L. a_lo / a_hi: this lane's byte offsets
+// inside an A chunk, b_lane inside a weight chunk.
 template <int AFMT, bool HALF>
-DSV4_DEV void big_read(BigFrag<AFMT, HALF>& F, const uint8_t* L, const uint8_t* S, int q0, int wm, const int* brow0,
-                       int r32, int g2, int a_lo, int a_hi, int b_lane) {
+DSV4_DEV void big_read(BigFrag<AFMT, HALF>& F, const uint8_t* L, int wm, const int* brow0, int r32, int a_lo,
+                       int a_hi, int b_lane) {
   using C = Big<AFMT, HALF>;
 #pragma unroll
-  for (int nt = 0; nt < Cfg<AFMT, HALF>::WT; ++nt) {
-    F.b[nt] = *(const v4i*)(L + (C::ACH + brow0[nt] / 32) * 1024 + b_lane);
-    F.sb[nt] = scale_byte<AFMT, HALF, true>(S, brow0[nt] + r32, q0 + g2);
-  }
+  for (int nt = 0; nt < Cfg<AFMT, HALF>::WT; ++nt) F.b[nt] = *(const v4i*)(L + (C::ACH + brow0[nt] / 32) * 1024 + b_lane);
 #pragma unroll
   for (int mt = 0; mt < Cfg<AFMT, HALF>::TT; ++mt) {
     const int row0 = (Cfg<AFMT, HALF>::BM / Cfg<AFMT, HALF>::WM) * wm + 32 * mt;
@@ -205,7 +194,58 @@ DSV4_DEV void big_read(BigFrag<AFMT, HALF>& F, const uint8_t* L, const uint8_t* 
     } else {
       F.lo[mt] = *(const v4i*)(L + (row0 / 32) * 1024 + a_lo);
     }
-    F.sa[mt] = scale_byte<AFMT, HALF, false>(S, row0 + r32, q0 + g2);
+  }
+}
+
+// Scales of a group of four stages 4j .. 4j + 3 for this wave's tiles. A super-stage
+// buffer holds, per A row and per weight row, the row's 32 E8M0 bytes of the 1024 k as
+// two 16-byte pieces, half-major ([A rows][weight rows], each [half][row] x 16 bytes).
+// Stage s of a super-stage uses, in lane (r32, g2), the row's byte q = 2 (s % 16) + g2:
+// byte 2 (s % 8) + g2 of its piece s / 8. The group's bytes
+// for both g2 are the 8 bytes at 2 (s % 8) (8-byte aligned): one ds_read_b64 per tile
+// per four stages instead of one byte read per tile per stage. Shifted right by 8 g2,
+// stage 4j + i's byte sits at bit 16 (i % 2) of word i / 2, which the MFMA picks with
+// its scale byte select (op_sel = 2 (i % 2)).
+template <int AFMT, bool HALF>
+struct BigScl {
+  uint64_t b[Cfg<AFMT, HALF>::WT], a[Cfg<AFMT, HALF>::TT];
+};
+template <int AFMT, bool HALF>
+struct BigSclW {
+  uint32_t b[Cfg<AFMT, HALF>::WT][2], a[Cfg<AFMT, HALF>::TT][2];
+};
+
+// Reads the raw scale groups of stages s0 .. s0 + 3 (s0 % 4 == 0, the stage within its
+// super-stage) from super-stage buffer S.
+template <int AFMT, bool HALF>
+DSV4_DEV void big_read_scales(BigScl<AFMT, HALF>& R, const uint8_t* S, int s0, int wm, const int* brow0, int r32) {
+  constexpr int kBM = Cfg<AFMT, HALF>::BM;
+  const int off = 2 * (s0 & 7), half = s0 >> 3;  // byte within the row's 16-byte piece `half`
+#pragma unroll
+  for (int nt = 0; nt < Cfg<AFMT, HALF>::WT; ++nt)
+    R.b[nt] = *(const uint64_t*)(S + kBM * 32 + (half * kBN + brow0[nt] + r32) * 16 + off);
+#pragma unroll
+  for (int mt = 0; mt < Cfg<AFMT, HALF>::TT; ++mt) {
+    const int row0 = (kBM / Cfg<AFMT, HALF>::WM) * wm + 32 * mt;
+    R.a[mt] = *(const uint64_t*)(S + (half * kBM + row0 + r32) * 16 + off);
+  }
+}
+
+// This lane's scale words of a group: its bytes (g2) moved to bits 0, 16 of two words.
+template <int AFMT, bool HALF>
+DSV4_DEV void big_scale_words(BigSclW<AFMT, HALF>& W, const BigScl<AFMT, HALF>& R, int g2) {
+  const int sh = 8 * g2;
+#pragma unroll
+  for (int nt = 0; nt < Cfg<AFMT, HALF>::WT; ++nt) {
+    const uint64_t v = R.b[nt] >> sh;
+    W.b[nt][0] = (uint32_t)v;
+    W.b[nt][1] = (uint32_t)(v >> 32);
+  }
+#pragma unroll
+  for (int mt = 0; mt < Cfg<AFMT, HALF>::TT; ++mt) {
+    const uint64_t v = R.a[mt] >> sh;
+    W.a[mt][0] = (uint32_t)v;
+    W.a[mt][1] = (uint32_t)(v >> 32);
   }
 }
 
@@ -213,10 +253,11 @@ DSV4_DEV void big_read(BigFrag<AFMT, HALF>& F, const uint8_t* L, const uint8_t* 
 // matrix pipe with FP8 A) followed by one of the stage's loads and two of the next
 // stage's fragment reads, so the LDS and the memory pipe work under the MFMAs and
 // the reads are done long before the next barrier waits for them.
-template <int AFMT, bool HALF>
+template <int AFMT, bool HALF, int I>
 DSV4_DEV void big_sched() {
   using G = Cfg<AFMT, HALF>;
-  constexpr int kReads = 2 * G::WT + (AFMT == 0 ? 3 : 2) * G::TT;  // ds_reads of big_read
+  // ds_reads of big_read (+ big_read_scales in the last stage of a group)
+  constexpr int kReads = G::WT + (AFMT == 0 ? 2 : 1) * G::TT + (I == 3 ? G::WT + G::TT : 0);
 #pragma unroll
   for (int i = 0; i < G::TT * G::WT; ++i) {
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                      // MFMA
@@ -229,8 +270,8 @@ DSV4_DEV void big_sched() {
 // operand and the activations its B operand, so accumulator (tt, wt) holds weight
 // columns x tokens: register r of lane l = weight column 8(r/4) + 4(l/32) + r%4 of
 // weight tile wt, token l%32 of token tile tt (the E4M3 B layout is the A layout).
-template <int AFMT, bool HALF>
-DSV4_DEV void big_mfma(typename Big<AFMT, HALF>::Acc& acc, const BigFrag<AFMT, HALF>& F) {
+template <int AFMT, bool HALF, int I>
+DSV4_DEV void big_mfma(typename Big<AFMT, HALF>::Acc& acc, const BigFrag<AFMT, HALF>& F, const BigSclW<AFMT, HALF>& W) {
 #pragma unroll
   for (int tt = 0; tt < Cfg<AFMT, HALF>::TT; ++tt) {
     const v4i lo = F.lo[tt];
@@ -239,8 +280,10 @@ DSV4_DEV void big_mfma(typename Big<AFMT, HALF>::Acc& acc, const BigFrag<AFMT, H
 #pragma unroll
     for (int wt = 0; wt < Cfg<AFMT, HALF>::WT; ++wt) {
       const v8i wf = v8i{F.b[wt].x, F.b[wt].y, F.b[wt].z, F.b[wt].w, 0, 0, 0, 0};
-      acc[tt][wt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf, xf, acc[tt][wt], 4, AFMT == 0 ? 0 : 4, 0,
-                                                                   F.sb[wt], 0, F.sa[tt]);
+      // stage I of the scale group: word I / 2, byte 2 (I % 2)
+      acc[tt][wt] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf, xf, acc[tt][wt], 4, AFMT == 0 ? 0 : 4,
+                                                                   2 * (I & 1), W.b[wt][I >> 1], 2 * (I & 1),
+                                                                   W.a[tt][I >> 1]);
     }
   }
 }
@@ -560,32 +603,41 @@ __global__ __launch_bounds__((Cfg<AFMT, HALF>::NT), (Cfg<AFMT, HALF>::WGS)) void
     for (int t = 0; t < C::NB; ++t) big_dma_stage<AFMT, HALF>(lds + t * C::STAGE, a_src, b_src, wave, bj, bg, t);
     wait_loads_barrier<C::L * (C::NB - 1)>();
     BigFrag<AFMT, HALF> f0, f1;
-    big_read<AFMT, HALF>(f0, lds, lds + C::AS_OFF, 0, wm, brow0, r32, g2, a_lo, a_hi, b_lane);
+    BigScl<AFMT, HALF> sr;   // raw scales of the next group of four stages
+    BigSclW<AFMT, HALF> sw;  // this lane's scale words of the current group
+    big_read<AFMT, HALF>(f0, lds, wm, brow0, r32, a_lo, a_hi, b_lane);
+    big_read_scales<AFMT, HALF>(sr, lds + C::AS_OFF, 0, wm, brow0, r32);
     int slot = 0;  // ring slot of stage s
-    // stage s: multiply Fc (stage s), read stage s + 1 into Fn
-#define DSV4_BIG_STEP(Fc, Fn)                                                                                  \
-  {                                                                                                            \
-    const int nslot = slot + 1 == C::NB ? 0 : slot + 1;                                                        \
-    wait_loads_barrier<C::L * (C::NB - 2)>();                                                                  \
-    big_dma_stage<AFMT, HALF>(lds + slot * C::STAGE, a_src, b_src, wave, bj, bg, min(s + C::NB, NST - 1));            \
-    const int s1 = s + 1;                                                                                      \
-    big_read<AFMT, HALF>(Fn, lds + nslot * C::STAGE, lds + C::AS_OFF + ((s1 / kSS) & 1) * C::SCL, 2 * (s1 % kSS),   \
-                   wm, brow0, r32, g2, a_lo, a_hi, b_lane);                                                    \
-    big_mfma<AFMT, HALF>(acc, Fc);                                                                                   \
-    big_sched<AFMT, HALF>();                                                                                         \
-    slot = nslot;                                                                                              \
-  }
+    // stage s (I = s % 4 of its scale group): multiply Fc (stage s), read stage s + 1
+    // into Fn and, in the group's last stage, the next group's scales
+    auto step = [&](auto I_, int s, BigFrag<AFMT, HALF>& Fc, BigFrag<AFMT, HALF>& Fn) __attribute__((always_inline)) {
+      constexpr int I = decltype(I_)::value;
+      const int nslot = slot + 1 == C::NB ? 0 : slot + 1;
+      wait_loads_barrier<C::L * (C::NB - 2)>();
+      if (I == 0) big_scale_words<AFMT, HALF>(sw, sr, g2);
+      big_dma_stage<AFMT, HALF>(lds + slot * C::STAGE, a_src, b_src, wave, bj, bg, min(s + C::NB, NST - 1));
+      const int s1 = s + 1;
+      big_read<AFMT, HALF>(Fn, lds + nslot * C::STAGE, wm, brow0, r32, a_lo, a_hi, b_lane);
+      if (I == 3) big_read_scales<AFMT, HALF>(sr, lds + C::AS_OFF + ((s1 / kSS) & 1) * C::SCL, s1 % kSS, wm, brow0, r32);
+      big_mfma<AFMT, HALF, I>(acc, Fc, sw);
+      big_sched<AFMT, HALF, I>();
+      slot = nslot;
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
 #pragma unroll 1
     for (int ss = 0; ss < NSS; ++ss) {
       big_dma_scales<AFMT, HALF>(lds, (ss + 1) & 1, sc_src, wave, min(ss + 1, NSS - 1));
 #pragma unroll 1
-      for (int s = kSS * ss; s < kSS * (ss + 1); ++s) {
-        DSV4_BIG_STEP(f0, f1);
-        ++s;
-        DSV4_BIG_STEP(f1, f0);
+      for (int s = kSS * ss; s < kSS * (ss + 1); s += 4) {
+        step(I0{}, s, f0, f1);
+        step(I1{}, s + 1, f1, f0);
+        step(I2{}, s + 2, f0, f1);
+        step(I3{}, s + 3, f1, f0);
       }
     }
-#undef DSV4_BIG_STEP
   }
   wait_loads_barrier<0>();  // every wave is done with the ring
 
@@ -740,7 +792,12 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_big_bf16_kernel(Dsv4GemmArgs 
         dma16(b_src[v] + boff, lds + t * bfk::STAGE + (bfk::ACH + wave * bfk::BV + v) * 1024);
     }
     int slot = 0, fill = bfk::NB - 1;
-    auto step = [&](int s) {
+    // weight scales of the current group of four stages, this lane's bytes (g2) moved to
+    // bits 16 i (stage 4j + i): one 8-byte read per tile per group (the row's bytes
+    // 2 (s % 8) .. + 7 of its piece (s % 16) / 8 hold both g2's bytes of the group)
+    uint64_t sr[G::WT];
+    auto step = [&](auto I_, int s) __attribute__((always_inline)) {
+      constexpr int I = decltype(I_)::value;  // s % 4
       wait_loads_barrier<bfk::L * (bfk::NB - 2)>();
       const int sl = min(s + bfk::NB - 1, NST - 1);
       uint8_t* fs = lds + fill * bfk::STAGE;
@@ -751,13 +808,18 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_big_bf16_kernel(Dsv4GemmArgs 
       for (int v = 0; v < bfk::BV; ++v) dma16(b_src[v] + boff, fs + (bfk::ACH + wave * bfk::BV + v) * 1024);
       const uint8_t* Ls = lds + slot * bfk::STAGE;
       const uint8_t* S = lds + bfk::AS_OFF + ((s / kSS) & 1) * bfk::SCL;
-      const int q = 2 * (s % kSS) + g2;  // this lane's 32-k block of the super-stage
+      if (I == 0) {
+        const int off = 2 * (s & 7), half = (s % kSS) >> 3;
+#pragma unroll
+        for (int wt = 0; wt < G::WT; ++wt)
+          sr[wt] = *(const uint64_t*)(S + (half * kBN + brow0[wt] + r32) * 16 + off) >> (8 * g2);
+      }
       v4i wf[G::WT];
       float wsc[G::WT];
 #pragma unroll
       for (int wt = 0; wt < G::WT; ++wt) {
         wf[wt] = *(const v4i*)(Ls + (bfk::ACH + brow0[wt] / 32) * 1024 + b_lane);
-        wsc[wt] = e8m0_scale(S[((q >> 4) * kBN + brow0[wt] + r32) * 16 + (q & 15)]);
+        wsc[wt] = e8m0_scale((uint32_t)(sr[wt] >> (16 * I)) & 0xffu);
       }
       bfx8 tk[2][G::TT];
 #pragma unroll
@@ -782,14 +844,27 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_big_bf16_kernel(Dsv4GemmArgs 
       slot = slot + 1 == bfk::NB ? 0 : slot + 1;
       fill = fill + 1 == bfk::NB ? 0 : fill + 1;
     };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    using I3 = std::integral_constant<int, 3>;
+    auto group = [&](int s) __attribute__((always_inline)) {
+      step(I0{}, s);
+      step(I1{}, s + 1);
+      step(I2{}, s + 2);
+      step(I3{}, s + 3);
+    };
 #pragma unroll 1
     for (int ss = 0; ss < NSS; ++ss) {
-      step(kSS * ss);
+      group(kSS * ss);
+      // the next super-stage's scales, once every wave is past stage 16 ss - 1 (the last
+      // reader of that buffer); older than the loads the waits of stages 16 ss + 4 ..
+      // leave in flight, so they have landed by stage 16 ss + 16
 #pragma unroll
       for (int v = 0; v < bfk::SV; ++v)
         dma16(sc_src[v] + min(ss + 1, NSS - 1) * 32, lds + bfk::AS_OFF + ((ss + 1) & 1) * bfk::SCL + (wave * bfk::SV + v) * 1024);
 #pragma unroll 1
-      for (int s = kSS * ss + 1; s < kSS * (ss + 1); ++s) step(s);
+      for (int s = kSS * ss + 4; s < kSS * (ss + 1); s += 4) group(s);
     }
   }
   wait_loads_barrier<0>();  // every wave is done with the ring
