@@ -490,7 +490,8 @@ __global__ __launch_bounds__((Cfg<AFMT, HALF>::NT), (Cfg<AFMT, HALF>::WGS)) void
   using G = Cfg<AFMT, HALF>;
   constexpr int kBM = G::BM, H = G::WT / 2;  // H: gate (and up) tiles per wave of gate/up
   __shared__ __attribute__((aligned(16))) uint8_t lds[C::LDS];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-DMA destinations in SGPRs
   const int wm = wave / G::WN, wn = wave % G::WN;
   int hb, nt;
   big_tile_of_block(hb, nt);  // hb: this workgroup's share of a hot-layout block
@@ -701,7 +702,8 @@ __global__ __launch_bounds__(512, 1) void moe_gemm_big_bf16_kernel(Dsv4GemmArgs 
   using G = CfgBf;
   constexpr int kBM = G::BM;
   __shared__ __attribute__((aligned(16))) uint8_t lds[bfk::LDS];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-DMA destinations in SGPRs
   const int wm = wave / G::WN, wn = wave % G::WN;
   int mb, nt;
   big_tile_of_block(mb, nt);
