@@ -361,8 +361,12 @@ def expert_table(experts, n_experts: int, device, tiled: bool = False) -> torch.
     ``experts`` maps expert id -> dict with keys ``w{1,2,3}{p,s}`` (device
     tensors, contiguous, any byte dtype). Missing experts get null entries.
     ``tiled``: the packed fields hold the MFMA-tiled layout (``tile_weights``);
-    their pointers carry the table's layout tag (bit 0)."""
+    their pointers carry the table's layout tag (bit 0). The returned tensor
+    holds references to the weight tensors, so they live as long as the table
+    (a table of raw pointers into freed tensors would read whatever the
+    allocator put there next)."""
     tab = torch.zeros((n_experts, 6), dtype=torch.int64)
+    refs = []
     items = experts.items() if hasattr(experts, "items") else enumerate(experts)
     for e, d in items:
         if d is None:
@@ -375,7 +379,10 @@ def expert_table(experts, n_experts: int, device, tiled: bool = False) -> torch.
             if t.data_ptr() % 16:
                 raise ValueError(f"expert {e} {k}: weights must be 16-byte aligned")
             tab[int(e), j] = t.data_ptr() | (_lib.TILED_WEIGHTS if tiled and k.endswith("p") else 0)
-    return tab.to(device)
+            refs.append(t)
+    out = tab.to(device)
+    out._dsv4_weights = refs
+    return out
 
 
 def gemm_gateup(afmt, a, a_scale, a_row_div, al: AlignResult, table, D, I, topk_w_flat, swiglu_limit, out=None):
