@@ -618,6 +618,10 @@ constexpr int tiled_a_buf_bytes() {
   return 16 * MT * ((AFMT == kAfmtBf16 ? 512 : AFMT == 0 ? 256 : 128) + 16);
 }
 
+// Row pitch of the bf16-activation kernel's weight-scale table in LDS (up to 32
+// bytes per row): 10 dwords, so the 16 rows one read touches sit on distinct banks.
+constexpr int kBfSclPitch = 40;
+
 // One M block of the tiled kernel. NTW: non-temporal weight loads (the block's
 // expert has no other M block, so nothing re-reads its weights).
 template <int AFMT, bool GATEUP, int NST, int MT, int NW, bool SH, bool NTW>
@@ -711,21 +715,61 @@ __attribute__((always_inline)) DSV4_DEV void tiled_block(const Dsv4GemmArgs& p,
     for (int t = 0; t < kNT; ++t) acc[mt][t] = v4f{0.f, 0.f, 0.f, 0.f};
 
   // bf16 activations: one weight stage in registers, whose half ji is reloaded
-  // with the next stage's as soon as it is dequantised; the weight rows' scale
-  // bytes come with each stage (a whole-K table per lane would not fit beside
-  // the dequantised fragments); the A tile moves in two halves (the other LDS
-  // buffer is free for the whole stage). Two waves per SIMD.
-  auto kloop_bf16 = [&](const uint8_t* const* btp, const uint8_t* const* bstp) {
+  // with the next stage's as soon as it is dequantised; the A tile moves in two
+  // halves (the other LDS buffer is free for the whole stage). Two waves per SIMD.
+  // The weight rows' scale bytes move SS stages at a time (8*SS bytes of each of
+  // the wave's 64 rows, two 16-byte loads per lane) into a wave-private LDS table
+  // that each stage reads its 2 bytes per tile from: fetched stage by stage they
+  // cost one L1->L2 request per row per stage, as many requests as the weight
+  // loads themselves, and a whole-K table per lane would not fit in registers
+  // beside the dequantised fragments.
+  auto kloop_bf16 = [&](const uint8_t* const* btp) {
     static_assert(LV % 2 == 0, "the A tile moves in two halves");
     constexpr int LH = LV / 2;
-    v4i lreg[LH];
+    constexpr int SS = NST < 4 ? NST : 4;  // stages per scale load
+    constexpr int CR = SS / 2;             // 16-byte scale chunks per row per load
+    uint8_t* stab = as_tab + __builtin_amdgcn_readfirstlane(wave) * (64 * kBfSclPitch);
+    // lane chunk i*64 + lane = part (i*64 + lane) % CR of table row (i*64 + lane) / CR
+    // = 16 t + r; chunk 1 (CR = 2) lies 32 table rows = two tiles further, at a
+    // uniform distance in the global rows (w3 instead of w1, or 32 rows of w2)
+    const int srow = lane / CR, spart = lane % CR, st = srow >> 4, sr = srow & 15;
+    const uint8_t* ssrc = (GATEUP ? (st < 2 ? ex.w1s : ex.w3s) + (int64_t)(col0 + 16 * (st & 1) + sr) * bsrow
+                                  : ex.w2s + (int64_t)(col0 + 16 * st + sr) * bsrow) +
+                          16 * spart;
+    const int64_t sstep = GATEUP ? (int64_t)((uintptr_t)ex.w3s - (uintptr_t)ex.w1s) : 32 * bsrow;
+    const int sdst = srow * kBfSclPitch + 16 * spart;
+    v4i sreg[CR];
+    auto sload = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < CR; ++i) sreg[i] = ld16((const uint8_t*)((uintptr_t)ssrc + i * sstep) + 8 * SS * s);
+    };
+    // the table rows are written and read by different lanes of the one wave,
+    // whose LDS accesses complete in order
+    auto sstore = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < CR; ++i) {
+        uint64_t* d = (uint64_t*)(stab + sdst + i * 32 * kBfSclPitch);
+        d[0] = (uint64_t)(uint32_t)sreg[i].x | ((uint64_t)(uint32_t)sreg[i].y << 32);
+        d[1] = (uint64_t)(uint32_t)sreg[i].z | ((uint64_t)(uint32_t)sreg[i].w << 32);
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
     BStageT<false> b;
+    auto sread = [&](int j) __attribute__((always_inline)) {
+#pragma unroll
+      for (int t = 0; t < kNT; ++t)
+        b.s[t] = *(const uint16_t*)(stab + (16 * t + r16) * kBfSclPitch + 8 * (j % SS) + 2 * g);
+    };
+    v4i lreg[LH];
 #pragma unroll
     for (int v = 0; v < LV; ++v)
       if (lon[v]) *(v4i*)&a_lds[0][ldst[v]] = ld16(lsrc[v]);
-    load_b<false, false, NTW>(b, btp, bstp, 0, g, lay);
-#pragma unroll
-    for (int t = 0; t < kNT; ++t) b.s[t] = ld_u16(bstp[t] + 2 * g);
+    load_b<false, false, NTW>(b, btp, nullptr, 0, g, lay);
+    sload(0);
+    sstore();
+    sread(0);
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < NST; ++j) {
@@ -736,6 +780,7 @@ __attribute__((always_inline)) DSV4_DEV void tiled_block(const Dsv4GemmArgs& p,
         for (int v = 0; v < LH; ++v)
           if (lon[v]) lreg[v] = ld16(lsrc[v] + (j + 1) * ASB);
       }
+      if (j % SS == SS - 2 && j + 2 < NST) sload(j / SS + 1);  // the next SS stages' scales
       bf16x8_t bw[kNT][4];
 #pragma unroll
       for (int ji = 0; ji < 2; ++ji) {
@@ -744,8 +789,8 @@ __attribute__((always_inline)) DSV4_DEV void tiled_block(const Dsv4GemmArgs& p,
 #pragma unroll
           for (int t = 0; t < kNT; ++t) b.d[t][ji] = ld16_w<NTW>(btp[t] + (j + 1) * lay.stage_stride + ji * lay.mfma_stride);
           if (ji == 1) {
-#pragma unroll
-            for (int t = 0; t < kNT; ++t) b.s[t] = ld_u16(bstp[t] + (j + 1) * 8 + 2 * g);
+            if (j % SS == SS - 1) sstore();  // stage j's bytes were read during stage j - 1
+            sread(j + 1);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -773,7 +818,7 @@ __attribute__((always_inline)) DSV4_DEV void tiled_block(const Dsv4GemmArgs& p,
     const uint8_t* const* btp = bt + t0;
     const uint8_t* const* bstp = bst + t0;
     if constexpr (ABF) {
-      kloop_bf16(btp, bstp);
+      kloop_bf16(btp);
       return;
     }
     // scales of the whole K range, loaded once: the weight rows' by their lanes
@@ -893,7 +938,7 @@ __global__ __launch_bounds__(64 * NW, (MT <= 4 && NW == 4 ? 2 : 1)) void moe_gem
   constexpr int BM = 16 * MT;
   constexpr int ASP = 8 * NST + 16;  // A scale table pitch (K / 32 + 16 bytes)
   __shared__ __attribute__((aligned(16))) uint8_t a_lds[2][tiled_a_buf_bytes<AFMT, MT>()];
-  __shared__ __attribute__((aligned(16))) uint8_t as_tab[AFMT == kAfmtBf16 ? 16 : BM * ASP];
+  __shared__ __attribute__((aligned(16))) uint8_t as_tab[AFMT == kAfmtBf16 ? NW * 64 * kBfSclPitch : BM * ASP];
   const int mb = blockIdx.y;
   const int npp = p.num_post_padded[0];
   if (mb * BM >= npp) return;
@@ -924,12 +969,19 @@ static void launch_nst_sh(const Dsv4GemmArgs& a, hipStream_t st) {
       hipLaunchKernelGGL((moe_gemm_kernel<1, GATEUP, NST, false>), grid, dim3(64 * kWaves), 0, st, a);
     return;
   }
-  // 4-wave workgroups (8-wave ones, sharing each A tile across twice the
-  // columns, measured no faster)
+  // 4-wave workgroups for E4M3 and E2M1 activations (8-wave ones, sharing each
+  // A tile across twice the columns, measured no faster); bf16 activations, with
+  // twice the A bytes of E4M3 per row, take 8-wave workgroups where the columns
+  // divide (1-3% faster at 512 and 2048 tokens, outputs bit-identical)
   const dim3 grid(a.N / (4 * cols_per_wave), a.max_blocks);
   if constexpr (!SH) {  // bf16 activations: 64-row blocks, routed experts only
     if (a.afmt == kAfmtBf16) {
-      hipLaunchKernelGGL((moe_gemm_tiled_kernel<kAfmtBf16, GATEUP, NST, 4, 4, false>), grid, dim3(256), 0, st, a);
+      if (a.N % (8 * cols_per_wave) == 0) {
+        const dim3 grid8(a.N / (8 * cols_per_wave), a.max_blocks);
+        hipLaunchKernelGGL((moe_gemm_tiled_kernel<kAfmtBf16, GATEUP, NST, 4, 8, false>), grid8, dim3(512), 0, st, a);
+      } else {
+        hipLaunchKernelGGL((moe_gemm_tiled_kernel<kAfmtBf16, GATEUP, NST, 4, 4, false>), grid, dim3(256), 0, st, a);
+      }
       return;
     }
   }
