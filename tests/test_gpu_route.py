@@ -83,7 +83,10 @@ def _check(out_w, out_ids, ref_w, ref_ids, scores, bias, K):
 @pytest.mark.parametrize("T,D,E,K,scoring,use_bias,renorm,xdtype", [
     (8, 4096, 256, 8, "sqrtsoftplus", True, True, "bf16"),     # decode
     (64, 4096, 256, 8, "softmax", True, True, "bf16"),
-    (2048, 4096, 256, 8, "sigmoid", False, True, "bf16"),      # prefill, no split-K
+    (2048, 4096, 256, 8, "sigmoid", False, True, "bf16"),      # prefill: 8-wave groups over 256 experts, x in LDS
+    (512, 2048, 256, 8, "softmax", True, True, "fp32"),        # the same with fp32 x
+    (256, 1024, 96, 6, "sqrtsoftplus", True, True, "bf16"),    # 64x32 tiles per wave, 512-k chunks, loads 3 steps ahead
+    (256, 768, 64, 4, "sigmoid", False, True, "fp32"),         # 64x32 tiles, a 768-k chunk: one step ahead
     (1, 4096, 256, 6, "sqrtsoftplus", True, True, "fp32"),
     (37, 1024, 48, 5, "softmax", False, True, "fp32"),         # E not a multiple of 64, ragged T
     (300, 2048, 512, 8, "sqrtsoftplus", True, False, "bf16"),
